@@ -1,0 +1,201 @@
+/*
+ * mlora.h — C ABI of the MI355X (gfx950) grouped MoE-LoRA operator library, libmlora.so.
+ *
+ * Every entry point is plain C: raw device pointers, element counts and element strides, a HIP
+ * stream passed as `void*` (NULL = the default stream), and an `int` status (0 = success).  On a
+ * non-zero status `mlora_last_error()` returns a message naming the argument or condition that was
+ * refused; the message is per host thread.  No entry point allocates device memory: a scratch
+ * buffer, where one is needed, is passed in by the caller and its required size is returned by a
+ * `*_workspace_bytes` query.  Nothing synchronises the host with the device; all work is enqueued
+ * on the given stream in order.
+ *
+ * Dtype codes (`MLORA_DT_*`) describe element types of tensors whose type can vary.
+ *
+ * Reference interfaces replaced (paths into thinkube/meepsquared; `TF:` = transformers 5.x):
+ *   routing     — TF:models/qwen3_moe/modeling_qwen3_moe.py:258-267 (router top-k softmax) and
+ *                 src/meepsquared/_moe.py:77-87 (sort, histc, cumsum offsets, sentinel mask)
+ *   tile map    — src/meepsquared/_grouped.py:83-103 (max_tiles, tile_map)
+ *   products    — src/meepsquared/_grouped.py:120-221 (_grouped_gemm_kernel) via _launch :313-345
+ *   reduction   — src/meepsquared/_grouped.py:232-256 (_grouped_reduce_kernel) via _reduce :362-370
+ *   layer glue  — src/meepsquared/_moe.py:80-81 (gather), TF:integrations/moe.py:509-520 (SwiGLU gate),
+ *                 src/meepsquared/_moe.py:123-126 (weight, un-permute, sum over k)
+ *   fp8 stacks  — src/meepsquared/_fp8.py:68-79,111-134 (_grouped_scale_kernel, quantize_stack,
+ *                 dequantize_stack), extended with one scale per output row
+ *   nf4 stacks  — src/meepsquared/_vendor/axolotl/quantize.py:52-101,202-235 (the NF4 double-quant
+ *                 format, there for dense layers only), applied here to expert stacks
+ */
+#ifndef MLORA_H
+#define MLORA_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  MLORA_DT_BF16 = 0,
+  MLORA_DT_F32 = 1,
+  MLORA_DT_F16 = 2,
+  MLORA_DT_FP8_E4M3 = 3, /* OCP float8 e4m3fn, torch.float8_e4m3fn */
+  MLORA_DT_NF4 = 4       /* two 4-bit NF4 codes per byte, first element in the high nibble */
+};
+
+enum {
+  MLORA_SCALE_NONE = 0,
+  MLORA_SCALE_EXPERT = 1, /* scale[e]: one fp32 per expert (the reference's fp8 stacks) */
+  MLORA_SCALE_ROW = 2     /* scale[e * scale_se + o]: one fp32 per output row o of the stack */
+};
+
+/* Library identity and the last error of this host thread ("" when none). */
+const char* mlora_version(void);
+const char* mlora_last_error(void);
+
+/* ---------------------------------------------------------------------------------------------
+ * Routing
+ * ------------------------------------------------------------------------------------------- */
+
+/* Router: probs = softmax(logits, fp32) over E, the k largest (descending; equal values in
+ * ascending expert order), weights = probs (renorm=0) or probs / sum of the k (renorm=1), cast to
+ * w_dtype (MLORA_DT_BF16 or MLORA_DT_F32).  logits: (T, E) of logits_dtype (bf16/f16/f32) with
+ * row stride ld_logits; out_idx (T, k) int64; out_w (T, k).  E <= 1024, 1 <= k <= min(E, 64).
+ * Replaces TF:models/qwen3_moe/modeling_qwen3_moe.py:262-266 (Mixtral: TF:models/mixtral/
+ * modeling_mixtral.py:104-111). */
+int mlora_route_topk(const void* logits, int logits_dtype, int64_t ld_logits, int64_t T, int E, int k,
+                     int renorm, int64_t* out_idx, void* out_w, int w_dtype, void* stream);
+
+/* Scratch bytes mlora_route_sort needs for S ids over E experts. */
+size_t mlora_route_sort_workspace_bytes(int64_t S, int E);
+
+/* Counting sort of S expert ids (int64; an id outside [0, E) is a sentinel and sorts to the tail).
+ * perm (S,) int64: the stable order, perm[p] = flat index of the p-th row in expert order;
+ * inv (S,) int64: inv[perm[p]] = p (may be NULL); offsets (E,) int32: the end of each expert's
+ * rows (cumsum of the per-expert counts, sentinels excluded).  When tile_expert is not NULL the
+ * tile map of `mlora_tile_map` for (offsets, rows=S, block_m, max_tiles) is written as well.  E <= 2048.
+ * Replaces src/meepsquared/_moe.py:77-87 (torch.sort, histc, cumsum) and _grouped.py:88-103. */
+int mlora_route_sort(const int64_t* ids, int64_t S, int E, int64_t* perm, int64_t* inv, int32_t* offsets,
+                     int block_m, int32_t* tile_expert, int32_t* tile_row, int32_t* tiles, int64_t max_tiles,
+                     void* workspace, size_t workspace_bytes, void* stream);
+
+/* The tile map of src/meepsquared/_grouped.py:88-103: each expert's rows cut into block_m-row
+ * tiles; tile_expert/tile_row (max_tiles,) int32, tiles a single int32 (the real count).  Spare
+ * entries hold the last expert and the row the reference's formula gives.  E <= 4096. */
+int mlora_tile_map(const int32_t* offsets, int E, int64_t rows, int block_m, int32_t* tile_expert,
+                   int32_t* tile_row, int32_t* tiles, int64_t max_tiles, void* stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * The grouped product with the fused LoRA (forward and input-gradient passes)
+ * ------------------------------------------------------------------------------------------- */
+
+/* out[row, n] = c · sum_k x[row, k] W_e[k, n] + scaling · bf16(x[row,:] · A_e)[:] · B_e[:, n] + bias[e, n]
+ * for every row of expert e (rows offsets[e-1] .. offsets[e]-1; rows past offsets[E-1] untouched).
+ *   x      (rows, K) bf16, row stride ldx, unit column stride, ldx % 8 == 0, 16-byte aligned.
+ *   w      the stack addressed as W_e[k, n] = w[e*w_se + k*w_sk + n*w_sn], w_sk == 1 or w_sn == 1,
+ *          in w_dtype: MLORA_DT_BF16, MLORA_DT_FP8_E4M3 or MLORA_DT_NF4 (NF4: a contiguous stack,
+ *          the strides in elements, blocks of 64 along the unit-stride axis, whose length is a
+ *          multiple of 64; nf4_absmax_q (uint8, one per block), nf4_absmax2 (fp32, one per 256
+ *          blocks), nf4_code2 (256 fp32, the second-level code), nf4_offset: block b's absmax is
+ *          code2[absmax_q[b]] * absmax2[b / 256] + nf4_offset[0]; nf4_code (16 fp32) the NF4 code
+ *          book; all of these on the device).
+ *   c      1, scale[e] (MLORA_SCALE_EXPERT), or scale[e*scale_se + o] for output row o of the
+ *          stack (MLORA_SCALE_ROW); scale_on_k = 1 says the stack's output rows run along k here
+ *          (the input-gradient pass), 0 along n.
+ *   at, bt the LoRA factors as A_e^T and B_e^T, bf16: A_e[k, r] = at[e*at_se + r*at_sr + k] (k contiguous)
+ *          and B_e[r, n] = bt[e*bt_se + n*bt_sn + r] (r contiguous); rank is 16, 32, 48 or 64 (a
+ *          smaller rank is padded with zero rows/columns by the caller, as src/meepsquared/
+ *          _grouped.py:275-282 does); at == NULL: no adapters.
+ *   low    (rows, rank) bf16 row stride ldl, receives bf16(x · A_e) (NULL: not stored).
+ *   bias   (E, N) bf16 with expert stride bias_se, or NULL.
+ *   out    (rows, N) bf16, row stride ldo, unit column stride.
+ * K % 8 == 0, N % 8 == 0.  Replaces _grouped_gemm_kernel (src/meepsquared/_grouped.py:120-221). */
+int mlora_grouped_gemm(const void* x, int64_t ldx, int64_t rows, int K, int N,
+                       const void* w, int w_dtype, int64_t w_se, int64_t w_sk, int64_t w_sn,
+                       const float* scale, int scale_kind, int64_t scale_se, int scale_on_k,
+                       const uint8_t* nf4_absmax_q, const float* nf4_absmax2, const float* nf4_code2,
+                       const float* nf4_offset, const float* nf4_code,
+                       const void* at, int64_t at_se, int64_t at_sr,
+                       const void* bt, int64_t bt_se, int64_t bt_sn, int rank, float scaling,
+                       const void* bias, int64_t bias_se,
+                       void* out, int64_t ldo, void* low, int64_t ldl,
+                       const int32_t* offsets, int E, void* stream);
+
+/* out[e, n, r] = bf16(scaling · sum over expert e's rows of g[row, n] · l[row, r]), fp32
+ * accumulation in a fixed order, no atomics: the adapters' gradients.  g (rows, N) bf16 row stride
+ * ldg; l (rows, R) bf16 row stride ldl; out addressed out[e*o_se + n*o_sn + r*o_sr].  R <= 64.
+ * Replaces _grouped_reduce_kernel (src/meepsquared/_grouped.py:232-256). */
+int mlora_grouped_reduce(const void* g, int64_t ldg, const void* l, int64_t ldl, int64_t rows, int N, int R,
+                         float scaling, const int32_t* offsets, int E,
+                         void* out, int64_t o_se, int64_t o_sn, int64_t o_sr, void* stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * The layer around the products: gather, SwiGLU, combine (bf16 activations)
+ * ------------------------------------------------------------------------------------------- */
+
+/* out[p, :] = h[perm[p] / k, :] for p < offsets[E-1], zero for the sentinel rows after it.
+ * h (T, H) row stride ldh; out (S, H) contiguous.  H % 8 == 0.  Replaces _moe.py:80,85-87. */
+int mlora_gather_rows(const void* h, int64_t ldh, int64_t H, const int64_t* perm, int64_t S, int k,
+                      const int32_t* offsets, int E, void* out, void* stream);
+
+/* The gather's gradient: dh[t, :] = sum over j < k of dsel[inv[t*k + j], :] (rows at or past
+ * offsets[E-1] skipped), fp32 accumulation.  dsel (S, H) contiguous; dh (T, H) contiguous. */
+int mlora_gather_rows_backward(const void* dsel, int64_t H, const int64_t* inv, int64_t T, int k,
+                               const int32_t* offsets, int E, void* dh, void* stream);
+
+/* act[r, i] = silu(gu[r, i]) · gu[r, I + i] (gate first, as TF:integrations/moe.py:509-520).
+ * gu (S, 2I) contiguous, act (S, I) contiguous, I % 8 == 0. */
+int mlora_swiglu(const void* gu, int64_t S, int64_t I, void* act, void* stream);
+
+/* dgu from dact and gu: dgate = dact · up · silu'(gate), dup = dact · silu(gate). */
+int mlora_swiglu_backward(const void* gu, const void* dact, int64_t S, int64_t I, void* dgu, void* stream);
+
+/* out[t, :] = sum over j < k of bf16(y[inv[t*k+j], :] · w[t*k+j]) with fp32 accumulation; rows at
+ * or past offsets[E-1] (sentinels) contribute nothing.  y (S, H) contiguous, w (T*k) of w_dtype
+ * (MLORA_DT_BF16 or MLORA_DT_F32), out (T, H) contiguous.  Replaces _moe.py:123-126. */
+int mlora_combine(const void* y, int64_t H, const void* w, int w_dtype, const int64_t* inv, int64_t T, int k,
+                  const int32_t* offsets, int E, void* out, void* stream);
+
+/* The combine's gradients: dy[inv[t*k+j], :] = bf16(dout[t, :] · w[t*k+j]) (zero for sentinel
+ * rows) and dw[t*k+j] = sum_h dout[t, h] · y[inv[t*k+j], h] (zero for sentinel rows), in w_dtype. */
+int mlora_combine_backward(const void* dout, const void* y, int64_t H, const void* w, int w_dtype,
+                           const int64_t* inv, int64_t T, int k, const int32_t* offsets, int E,
+                           void* dy, void* dw, void* stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * Frozen stack formats
+ * ------------------------------------------------------------------------------------------- */
+
+/* fp8 e4m3 stack with fp32 scales: x (E, R, C) contiguous of x_dtype (bf16/f32).  group =
+ * MLORA_SCALE_EXPERT: one scale per expert over its R*C values; MLORA_SCALE_ROW with
+ * rows_on_last = 0: one per (e, r) over C values; rows_on_last = 1: one per (e, c) over R values
+ * (the stack (E, in, out), whose output rows are its columns).  scale = max(amax, 1e-12) / 448,
+ * q = e4m3(x / scale) rounded to nearest even.  Replaces _fp8.py:122-128 (one scale per expert). */
+int mlora_fp8_quantize(const void* x, int x_dtype, int64_t E, int64_t R, int64_t C, int group, int rows_on_last,
+                       uint8_t* q, float* scale, void* stream);
+
+/* y = fp8 · scale in y_dtype (bf16/f32), the same grouping.  Replaces _fp8.py:131-134. */
+int mlora_fp8_dequantize(const uint8_t* q, const float* scale, int64_t E, int64_t R, int64_t C, int group,
+                         int rows_on_last, void* y, int y_dtype, void* stream);
+
+/* Scratch bytes mlora_nf4_quantize needs for n values. */
+size_t mlora_nf4_workspace_bytes(int64_t n);
+
+/* NF4 with double quantization of x (n values, bf16/f32, n % 64 == 0), blocks of 64: absmax per
+ * block; offset = mean of the absmaxes; (absmax - offset) quantised with code2 in blocks of 256
+ * (absmax2 = max |absmax - offset| per 256 blocks, absmax_q = nearest code2 index); each value's
+ * code = nearest entry of `code` (16 fp32) to x / decoded absmax.  packed (n/2) uint8, absmax_q
+ * (n/64) uint8, absmax2 (ceil(n/64/256)) fp32, offset (1) fp32, all on the device. */
+int mlora_nf4_quantize(const void* x, int x_dtype, int64_t n, const float* code, const float* code2,
+                       uint8_t* packed, uint8_t* absmax_q, float* absmax2, float* offset,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
+/* y = code[nibble] · (code2[absmax_q[b]] · absmax2[b/256] + offset[0]) in y_dtype (bf16/f32). */
+int mlora_nf4_dequantize(const uint8_t* packed, const uint8_t* absmax_q, const float* absmax2,
+                         const float* offset, const float* code, const float* code2, int64_t n,
+                         void* y, int y_dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MLORA_H */

@@ -1,0 +1,266 @@
+"""The experts' products with their LoRA adapters, one kernel launch each, on MI355X (gfx950).
+
+The rows of x are sorted by expert; offsets[e] is the end of expert e's rows.  For every expert e
+and its rows x_e the forward computes
+
+    out_e = c_e · x_e @ W_e^T + s · bf16(x_e @ A_e^T) @ B_e^T + bias_e
+
+with the stack W as (experts, out, in) or, when is_transposed, (experts, in, out), in bf16, in
+fp8 e4m3 with one scale per expert or per output row (c_e), or in NF4 (`meepsquared_amd._nf4`);
+the adapters are PEFT's lhs and rhs factors in the stack's layout.  The kernel is
+`csrc/grouped_gemm.hip`, reached through the C ABI of `include/mlora.h`.
+
+This module keeps the interface of the reference's `src/meepsquared/_grouped.py`: BLOCK_M and
+RANK_MULTIPLE (:51-52), max_tiles and tile_map (:83-103), the stack-stride check and its
+ValueError (:264-272), the rank padding (:275-282), the adapters' roles (:285-310),
+grouped_linear (:348-359), the autograd Function with its gradient tuple (:373-405) and
+lora_linear (:408-417).  The per-expert float32 references (:420-444) are test oracles and live
+in the repository's `oracle/` package, not here.
+"""
+
+import torch
+
+from meepsquared_amd import _lib
+from meepsquared_amd._lib import call, ptr
+
+BLOCK_M = 128
+RANK_MULTIPLE = 16  # the kernel's low-rank MFMAs take the rank in blocks of 16
+
+
+def max_tiles(rows: int, experts: int, block_m: int = BLOCK_M) -> int:
+    """An upper bound on the tiles: every expert's last tile may be partial (_grouped.py:83-85)."""
+    return rows // block_m + experts
+
+
+def tile_map(offsets: torch.Tensor, rows: int, block_m: int = BLOCK_M):
+    """(tile_expert, tile_row, tiles) for `rows` rows sorted by expert, computed on the GPU.
+
+    offsets[e] is the end of expert e's rows (int32, on the device).  The two arrays have
+    max_tiles entries; tiles, a 0-d int32 tensor on the device, says how many are real.  Entries
+    beyond that hold the last expert.  Same values as src/meepsquared/_grouped.py:88-103.
+    The product kernel derives this map itself; this function exposes it.
+    """
+    _lib.require_gpu(offsets)
+    offsets = offsets.to(torch.int32).contiguous()
+    experts = offsets.numel()
+    n = max_tiles(rows, experts, block_m)
+    tile_expert = torch.empty(n, device=offsets.device, dtype=torch.int32)
+    tile_row = torch.empty(n, device=offsets.device, dtype=torch.int32)
+    tiles = torch.empty((), device=offsets.device, dtype=torch.int32)
+    call("mlora_tile_map", ptr(offsets), experts, rows, block_m, ptr(tile_expert), ptr(tile_row), ptr(tiles), n,
+         _lib.stream(offsets.device))
+    return tile_expert, tile_row, tiles
+
+
+class Nf4Stack:
+    """An expert stack held as NF4 with double quantisation (made by meepsquared_amd._nf4.quantize_stack)."""
+
+    def __init__(self, packed, absmax_q, absmax2, offset, code, code2, shape, dtype=torch.bfloat16):
+        self.packed, self.absmax_q, self.absmax2, self.offset = packed, absmax_q, absmax2, offset
+        self.code, self.code2 = code, code2
+        self.shape = torch.Size(shape)
+        self.dtype = dtype  # the dtype it dequantises to
+
+    @property
+    def device(self):
+        return self.packed.device
+
+    def dim(self):
+        return 3
+
+    def stride(self, d=None):
+        strides = (self.shape[1] * self.shape[2], self.shape[2], 1)
+        return strides if d is None else strides[d]
+
+
+def _stack_strides(weight, K: int, is_transposed: bool):
+    """(N, stride_e, stride_k, stride_n) of a stack addressed as (k, n); src/meepsquared/_grouped.py:264-272."""
+    if is_transposed:
+        if weight.shape[1] != K:
+            raise ValueError(f"a transposed stack (experts, in, out) with in={weight.shape[1]} does not take x with {K} columns")
+        return weight.shape[2], weight.stride(0), weight.stride(1), weight.stride(2)
+    if weight.shape[2] != K:
+        raise ValueError(f"a stack (experts, out, in) with in={weight.shape[2]} does not take x with {K} columns")
+    return weight.shape[1], weight.stride(0), weight.stride(2), weight.stride(1)
+
+
+def _padded_rank(factor: torch.Tensor, dim: int) -> torch.Tensor:
+    """The factor with its rank dimension padded with zeros to a multiple of RANK_MULTIPLE (_grouped.py:275-282)."""
+    pad = -factor.shape[dim] % RANK_MULTIPLE
+    if not pad:
+        return factor
+    shape = list(factor.shape)
+    shape[dim] = pad
+    return torch.cat([factor, factor.new_zeros(shape)], dim=dim)
+
+
+class _Adapters:
+    """PEFT's factors as the kernel reads them: A^T as (e, R, k) and B^T as (e, n, R), R the padded rank.
+
+    delta = lhs @ rhs in the stack's layout: (out, in) means lhs (out, rank) and rhs (rank, in),
+    so A = rhs^T and B = lhs^T; (in, out) means lhs (in, rank) and rhs (rank, out), so A = lhs and
+    B = rhs.  Roles as in src/meepsquared/_grouped.py:285-310.
+    """
+
+    def __init__(self, lhs, rhs, is_transposed):
+        self.rank = lhs.shape[2]
+        if is_transposed:
+            at, bt = lhs.transpose(1, 2), rhs.transpose(1, 2)
+        else:
+            at, bt = rhs, lhs
+        self.at = _padded_rank(at, 1).to(torch.bfloat16).contiguous()  # (e, R, k)
+        self.bt = _padded_rank(bt, 2).to(torch.bfloat16).contiguous()  # (e, n, R)
+        self.padded = self.at.shape[1]
+
+    def swapped(self):
+        """The adapters of the input-gradient product: B takes A's role and A B's (_grouped.py:304-310)."""
+        other = object.__new__(_Adapters)
+        other.rank, other.padded = self.rank, self.padded
+        other.at = self.bt.transpose(1, 2).contiguous()  # (e, R, n): B's rows become the new k
+        other.bt = self.at.transpose(1, 2).contiguous()  # (e, k, R)
+        return other
+
+
+def _scale_args(scale, weight, backward: bool):
+    """(scale, kind, stride_e, on_k): one scale per expert (E,) or per output row (E, out)."""
+    if scale is None:
+        return None, _lib.SCALE_NONE, 0, 0
+    _lib.require_gpu(scale)
+    scale = scale.to(torch.float32).contiguous()
+    if scale.dim() == 1:
+        if scale.numel() != weight.shape[0]:
+            raise ValueError(f"a per-expert scale needs {weight.shape[0]} values, got {scale.numel()}")
+        return scale, _lib.SCALE_EXPERT, 0, 0
+    if scale.dim() == 2 and scale.shape[0] == weight.shape[0]:
+        return scale, _lib.SCALE_ROW, scale.stride(0), int(backward)
+    raise ValueError(f"scale of shape {tuple(scale.shape)} is neither (experts,) nor (experts, out)")
+
+
+def _launch(x, weight, scale, offsets, is_transposed, adapters, scaling, bias, store_low, backward=False):
+    """One launch of the product kernel. Returns (out, low), low None without adapters or store_low."""
+    _lib.require_gpu(x, offsets)
+    if x.dtype != torch.bfloat16:
+        raise TypeError(f"x is {x.dtype}; the kernel computes in bf16")
+    rows, K = x.shape
+    if x.stride(1) != 1 or x.stride(0) % 8 or x.data_ptr() % 16:
+        x = x.contiguous()
+    N, w_se, w_sk, w_sn = _stack_strides(weight, K, is_transposed)
+    out = torch.empty((rows, N), device=x.device, dtype=x.dtype)
+    R = adapters.padded if adapters is not None else 0
+    low = torch.empty((rows, R), device=x.device, dtype=torch.bfloat16) if (adapters is not None and store_low) else None
+    if rows == 0:
+        return out, low
+    offsets = offsets if offsets.dtype == torch.int32 else offsets.to(torch.int32)
+    offsets = offsets.contiguous()
+    scale, scale_kind, scale_se, scale_on_k = _scale_args(scale, weight, backward)
+    nf4 = (None,) * 5
+    if isinstance(weight, Nf4Stack):
+        w_ptr, w_dtype = ptr(weight.packed), _lib.DT_NF4
+        nf4 = (ptr(weight.absmax_q), ptr(weight.absmax2), ptr(weight.code2), ptr(weight.offset), ptr(weight.code))
+    else:
+        _lib.require_gpu(weight)
+        if weight.dtype not in (torch.bfloat16, torch.float8_e4m3fn):
+            raise TypeError(f"a stack in {weight.dtype}: the kernel takes bf16, float8_e4m3fn or NF4")
+        w_ptr, w_dtype = ptr(weight), _lib.dtype_code(weight.dtype)
+    if bias is not None:
+        bias = bias.to(torch.bfloat16)
+        if bias.stride(-1) != 1:
+            bias = bias.contiguous()
+    at = bt = None
+    if adapters is not None:
+        at, bt = adapters.at, adapters.bt
+    call("mlora_grouped_gemm",
+         ptr(x), x.stride(0), rows, K, N,
+         w_ptr, w_dtype, w_se, w_sk, w_sn,
+         ptr(scale), scale_kind, scale_se, scale_on_k,
+         *nf4,
+         ptr(at), at.stride(0) if at is not None else 0, at.stride(1) if at is not None else 0,
+         ptr(bt), bt.stride(0) if bt is not None else 0, bt.stride(1) if bt is not None else 0,
+         R, float(scaling),
+         ptr(bias), bias.stride(0) if bias is not None else 0,
+         ptr(out), out.stride(0), ptr(low), low.stride(0) if low is not None else 0,
+         ptr(offsets), offsets.numel(), _lib.stream(x.device))
+    return out, low
+
+
+def grouped_linear(x: torch.Tensor, weight, offsets: torch.Tensor, is_transposed: bool,
+                   block_m: int = BLOCK_M, products_fp8=None) -> torch.Tensor:
+    """x (rows, in) by the stack (experts, out, in), or (experts, in, out) when is_transposed, per expert group.
+
+    offsets (experts,) int32 on the device: the end of each expert's rows.  Returns (rows, out) in
+    x's dtype.  A stack in fp8 is converted in registers without a scale: the caller folds the
+    scale in.  The base product alone (src/meepsquared/_grouped.py:348-359); block_m is accepted
+    for the reference's signature, the kernel's own tiling is fixed.
+    """
+    _check_products(products_fp8)
+    return _launch(x, weight, None, offsets, is_transposed, None, 1.0, None, False)[0]
+
+
+def _check_products(products_fp8):
+    if products_fp8:
+        raise NotImplementedError("fp8 products (activations quantised to e4m3 on the MFMA) are not built; "
+                                  "fp8 stacks are decoded to bf16 in registers")
+
+
+def _reduce(g: torch.Tensor, low: torch.Tensor, offsets: torch.Tensor, scaling: float) -> torch.Tensor:
+    """(experts, N, R) bf16: scaling · sum over each expert's rows of g^T @ low (_grouped.py:362-370)."""
+    experts = offsets.numel()
+    rows, N = g.shape
+    R = low.shape[1]
+    if g.stride(1) != 1 or g.stride(0) % 8 or g.data_ptr() % 16:
+        g = g.contiguous()
+    out = torch.empty((experts, N, R), device=g.device, dtype=torch.bfloat16)
+    call("mlora_grouped_reduce", ptr(g), g.stride(0), ptr(low), low.stride(0), rows, N, R, float(scaling),
+         ptr(offsets), experts, ptr(out), out.stride(0), out.stride(1), out.stride(2), _lib.stream(g.device))
+    return out
+
+
+class _LoraGroupedProduct(torch.autograd.Function):
+    """The experts' product with the adapters; gradients for x and the adapters, none for the frozen stack."""
+
+    @staticmethod
+    def forward(ctx, x, weight, scale, offsets, is_transposed, lhs, rhs, scaling, bias, products_fp8):
+        _check_products(products_fp8)
+        offsets = offsets.to(torch.int32).contiguous()
+        adapters = _Adapters(lhs, rhs, is_transposed) if lhs is not None else None
+        out, low = _launch(x, weight, scale, offsets, is_transposed, adapters, scaling, bias, True)
+        ctx.save_for_backward(x, offsets, *((low,) if low is not None else ()))
+        ctx.weight = weight  # frozen: held as it is (an NF4 stack is not a tensor)
+        ctx.adapters, ctx.scale, ctx.is_transposed, ctx.scaling = adapters, scale, is_transposed, scaling
+        ctx.lhs_dtype = lhs.dtype if lhs is not None else None
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        x, offsets, *rest = ctx.saved_tensors
+        adapters, weight = ctx.adapters, ctx.weight
+        grad_out = grad_out.to(torch.bfloat16).contiguous()
+        if adapters is None:
+            grad_x, _ = _launch(grad_out, weight, ctx.scale, offsets, not ctx.is_transposed, None, 1.0, None, False,
+                                backward=True)
+            return grad_x, None, None, None, None, None, None, None, None, None
+        low = rest[0]
+        # grad_x = grad @ W (the stack read the other way) + scaling · bf16(grad @ B^T) @ A^T
+        grad_x, low2 = _launch(grad_out, weight, ctx.scale, offsets, not ctx.is_transposed, adapters.swapped(),
+                               ctx.scaling, None, True, backward=True)
+        grad_a = _reduce(x, low2, offsets, ctx.scaling)        # (experts, in, R): A's gradient, addressed (k, r)
+        grad_b = _reduce(grad_out, low, offsets, ctx.scaling)  # (experts, out, R): B's gradient, addressed (n, r)
+        rank = adapters.rank
+        if ctx.is_transposed:  # A = lhs (in, rank), B = rhs (rank, out)
+            grad_lhs, grad_rhs = grad_a[:, :, :rank], grad_b.transpose(1, 2)[:, :rank, :]
+        else:  # A = rhs^T, B = lhs^T
+            grad_lhs, grad_rhs = grad_b[:, :, :rank], grad_a.transpose(1, 2)[:, :rank, :]
+        if ctx.lhs_dtype is not None and ctx.lhs_dtype != torch.bfloat16:
+            grad_lhs, grad_rhs = grad_lhs.to(ctx.lhs_dtype), grad_rhs.to(ctx.lhs_dtype)
+        return grad_x, None, None, None, None, grad_lhs, grad_rhs, None, None, None
+
+
+def lora_linear(x, weight, scale, offsets, is_transposed: bool, lhs=None, rhs=None, scaling: float = 1.0, bias=None,
+                products_fp8=None):
+    """The experts' product of x with the stack, the adapters (PEFT's lhs, rhs, scaling) and the bias stack (experts, out).
+
+    scale is the fp8 stack's scale: (experts,) as the reference holds it, or (experts, out), one per
+    output row; None for a bf16 or NF4 stack.  Same signature and gradients as
+    src/meepsquared/_grouped.py:408-417.
+    """
+    return _LoraGroupedProduct.apply(x, weight, scale, offsets, is_transposed, lhs, rhs, scaling, bias, products_fp8)

@@ -1,0 +1,74 @@
+// Shared definitions of the gfx950 kernels: vector types, conversions, wave primitives, errors.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+#include "../../include/mlora.h"
+
+namespace mlora {
+
+typedef __bf16 bf16;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kWave = 64;
+
+// ---- error reporting (per host thread), defined in api.hip ----
+int fail(const char* fmt, ...);
+void clear_error();
+// status of the last launch on the calling thread; 0 or a failure recorded with the kernel's name
+int launch_status(const char* what);
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// ---- conversions ----
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
+
+// two bf16 packed in a dword (element 0 in the low half) from two floats, rounded to nearest even
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  bf16 a = (bf16)lo, b = (bf16)hi;
+  return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+}
+
+__device__ __forceinline__ float round_bf16(float v) { return (float)(bf16)v; }
+
+// OCP e4m3fn byte to fp32: exact (every e4m3 value is a bf16/fp32 value).  0x7f/0xff (NaN) are not
+// produced by the quantisers here and decode as 480.
+__device__ __forceinline__ float fp8_e4m3_to_f32(uint32_t byte) {
+  uint32_t s = (byte & 0x80u) << 24;
+  uint32_t e = (byte >> 3) & 0xFu;
+  uint32_t m = byte & 0x7u;
+  float normal = __uint_as_float(s | ((e + 120u) << 23) | (m << 20));
+  float sub = __uint_as_float(s | __float_as_uint((float)m * 0.001953125f));  // m * 2^-9
+  return e ? normal : sub;
+}
+
+// ---- wave primitives (wave64) ----
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    uint64_t w = __shfl_xor((unsigned long long)v, o, kWave);
+    v = w > v ? w : v;
+  }
+  return v;
+}
+
+__device__ __forceinline__ int lane_id() { return __lane_id(); }
+
+}  // namespace mlora

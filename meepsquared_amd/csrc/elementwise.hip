@@ -1,0 +1,270 @@
+// The layer's data movement and elementwise steps around the grouped products: the gather of the
+// tokens' rows into expert order, the SwiGLU gate, and the weighted combine back to tokens, with
+// their gradients.  All of them are bound by HBM bandwidth: rows move as 16-byte vectors, every
+// sum runs in fp32 in a fixed order (no atomics), so results are the same every run.
+//
+// Reference behaviour (paths into thinkube/meepsquared; TF: = transformers):
+//   gather   src/meepsquared/_moe.py:80,85-87  selected = h[perm // k], sentinel rows zeroed
+//   SwiGLU   TF:integrations/moe.py:509-520     gate, up = chunk(2); silu(gate) * up
+//   combine  src/meepsquared/_moe.py:123-126   (out * w)[inverse].view(T, k, H).sum(1)
+#include "common.hpp"
+
+namespace mlora {
+
+__device__ __forceinline__ void unpack8(const u32x4& v, float* f) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = bf16_bits_to_f32(v[i] & 0xFFFFu);
+    f[2 * i + 1] = bf16_bits_to_f32(v[i] >> 16);
+  }
+}
+__device__ __forceinline__ u32x4 pack8(const float* f) {
+  u32x4 v;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = pack_bf16x2(f[2 * i], f[2 * i + 1]);
+  return v;
+}
+
+template <typename TW>
+__device__ __forceinline__ float load_w(const TW* w, int64_t i);
+template <>
+__device__ __forceinline__ float load_w<float>(const float* w, int64_t i) { return w[i]; }
+template <>
+__device__ __forceinline__ float load_w<bf16>(const bf16* w, int64_t i) { return (float)w[i]; }
+
+// ---- gather: one 16-byte vector per thread, grid-stride over (row, vector) ----
+__global__ __launch_bounds__(256) void gather_rows_kernel(const u32x4* __restrict__ h, int64_t ldh_v, int64_t Hv,
+                                                          const int64_t* __restrict__ perm, int64_t S, int k,
+                                                          const int32_t* __restrict__ offsets, int E,
+                                                          u32x4* __restrict__ out) {
+  const int64_t valid = offsets[E - 1];
+  const int64_t total = S * Hv;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t p = i / Hv, c = i - p * Hv;
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (p < valid) v = h[(perm[p] / k) * ldh_v + c];
+    out[i] = v;
+  }
+}
+
+// ---- the gather's gradient: per token, the sum of its k rows ----
+__global__ __launch_bounds__(256) void gather_rows_backward_kernel(const u32x4* __restrict__ dsel, int64_t Hv,
+                                                                   const int64_t* __restrict__ inv, int64_t T, int k,
+                                                                   const int32_t* __restrict__ offsets, int E,
+                                                                   u32x4* __restrict__ dh) {
+  const int64_t valid = offsets[E - 1];
+  const int64_t total = T * Hv;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t t = i / Hv, c = i - t * Hv;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < k; ++j) {
+      const int64_t p = inv[t * k + j];
+      if (p >= valid) continue;
+      float f[8];
+      unpack8(dsel[p * Hv + c], f);
+#pragma unroll
+      for (int q = 0; q < 8; ++q) acc[q] += f[q];
+    }
+    dh[i] = pack8(acc);
+  }
+}
+
+// ---- SwiGLU ----
+__device__ __forceinline__ float sigmoidf_(float g) { return 1.0f / (1.0f + expf(-g)); }
+
+__global__ __launch_bounds__(256) void swiglu_kernel(const u32x4* __restrict__ gu, int64_t S, int64_t Iv,
+                                                     u32x4* __restrict__ act) {
+  const int64_t total = S * Iv;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i / Iv, c = i - r * Iv;
+    float g[8], u[8], o[8];
+    unpack8(gu[r * 2 * Iv + c], g);
+    unpack8(gu[r * 2 * Iv + Iv + c], u);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) o[q] = g[q] * sigmoidf_(g[q]) * u[q];
+    act[i] = pack8(o);
+  }
+}
+
+__global__ __launch_bounds__(256) void swiglu_backward_kernel(const u32x4* __restrict__ gu,
+                                                              const u32x4* __restrict__ dact, int64_t S, int64_t Iv,
+                                                              u32x4* __restrict__ dgu) {
+  const int64_t total = S * Iv;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i / Iv, c = i - r * Iv;
+    float g[8], u[8], d[8], dg[8], du[8];
+    unpack8(gu[r * 2 * Iv + c], g);
+    unpack8(gu[r * 2 * Iv + Iv + c], u);
+    unpack8(dact[i], d);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const float sg = sigmoidf_(g[q]);
+      const float silu = g[q] * sg;
+      du[q] = d[q] * silu;
+      dg[q] = d[q] * u[q] * sg * (1.0f + g[q] * (1.0f - sg));
+    }
+    dgu[r * 2 * Iv + c] = pack8(dg);
+    dgu[r * 2 * Iv + Iv + c] = pack8(du);
+  }
+}
+
+// ---- combine: per token, sum over its k rows of bf16(y * w) ----
+template <typename TW>
+__global__ __launch_bounds__(256) void combine_kernel(const u32x4* __restrict__ y, int64_t Hv,
+                                                      const TW* __restrict__ w, const int64_t* __restrict__ inv,
+                                                      int64_t T, int k, const int32_t* __restrict__ offsets, int E,
+                                                      u32x4* __restrict__ out) {
+  constexpr bool kBf16Weights = sizeof(TW) == 2;
+  const int64_t valid = offsets[E - 1];
+  const int64_t total = T * Hv;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t t = i / Hv, c = i - t * Hv;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < k; ++j) {
+      const int64_t p = inv[t * k + j];
+      if (p >= valid) continue;
+      const float wt = load_w(w, t * k + j);
+      float f[8];
+      unpack8(y[p * Hv + c], f);
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        // with bf16 weights the reference's product is a bf16 tensor; with fp32 weights it is fp32
+        const float prod = f[q] * wt;
+        acc[q] += kBf16Weights ? round_bf16(prod) : prod;
+      }
+    }
+    out[i] = pack8(acc);
+  }
+}
+
+// ---- the combine's gradients: one block per token ----
+template <typename TW>
+__global__ __launch_bounds__(256) void combine_backward_kernel(const u32x4* __restrict__ dout,
+                                                               const u32x4* __restrict__ y, int64_t Hv,
+                                                               const TW* __restrict__ w,
+                                                               const int64_t* __restrict__ inv, int64_t T, int k,
+                                                               const int32_t* __restrict__ offsets, int E,
+                                                               u32x4* __restrict__ dy, TW* __restrict__ dw) {
+  __shared__ float part[4];
+  const int64_t valid = offsets[E - 1];
+  const int64_t t = blockIdx.x;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  for (int j = 0; j < k; ++j) {
+    const int64_t p = inv[t * k + j];
+    const bool sentinel = p >= valid;
+    const float wt = load_w(w, t * k + j);
+    float dot = 0.f;
+    for (int64_t c = threadIdx.x; c < Hv; c += blockDim.x) {
+      float d[8], f[8], o[8];
+      unpack8(dout[t * Hv + c], d);
+      if (sentinel) {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) o[q] = 0.f;
+      } else {
+        unpack8(y[p * Hv + c], f);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          o[q] = d[q] * wt;
+          dot += d[q] * f[q];
+        }
+      }
+      dy[p * Hv + c] = pack8(o);
+    }
+    dot = wave_sum(dot);
+    if (lane == 0) part[wv] = dot;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      const float s = sentinel ? 0.f : ((part[0] + part[1]) + (part[2] + part[3]));
+      dw[t * k + j] = (TW)s;
+    }
+    __syncthreads();
+  }
+}
+
+static unsigned grid_for(int64_t total) {
+  int64_t g = (total + 255) / 256;
+  if (g > 256 * 64) g = 256 * 64;
+  return (unsigned)(g < 1 ? 1 : g);
+}
+
+}  // namespace mlora
+
+using namespace mlora;
+
+extern "C" int mlora_gather_rows(const void* h, int64_t ldh, int64_t H, const int64_t* perm, int64_t S, int k,
+                                 const int32_t* offsets, int E, void* out, void* stream) {
+  clear_error();
+  if (H % 8 || ldh % 8) return fail("gather_rows: H=%lld and ldh=%lld must be multiples of 8", (long long)H, (long long)ldh);
+  if (k < 1 || E < 1) return fail("gather_rows: k=%d, E=%d must be >= 1", k, E);
+  if (S == 0) return 0;
+  hipLaunchKernelGGL(gather_rows_kernel, dim3(grid_for(S * (H / 8))), dim3(256), 0, as_stream(stream),
+                     (const u32x4*)h, ldh / 8, H / 8, perm, S, k, offsets, E, (u32x4*)out);
+  return launch_status("gather_rows");
+}
+
+extern "C" int mlora_gather_rows_backward(const void* dsel, int64_t H, const int64_t* inv, int64_t T, int k,
+                                          const int32_t* offsets, int E, void* dh, void* stream) {
+  clear_error();
+  if (H % 8) return fail("gather_rows_backward: H=%lld must be a multiple of 8", (long long)H);
+  if (k < 1 || E < 1) return fail("gather_rows_backward: k=%d, E=%d must be >= 1", k, E);
+  if (T == 0) return 0;
+  hipLaunchKernelGGL(gather_rows_backward_kernel, dim3(grid_for(T * (H / 8))), dim3(256), 0, as_stream(stream),
+                     (const u32x4*)dsel, H / 8, inv, T, k, offsets, E, (u32x4*)dh);
+  return launch_status("gather_rows_backward");
+}
+
+extern "C" int mlora_swiglu(const void* gu, int64_t S, int64_t I, void* act, void* stream) {
+  clear_error();
+  if (I % 8) return fail("swiglu: I=%lld must be a multiple of 8", (long long)I);
+  if (S == 0) return 0;
+  hipLaunchKernelGGL(swiglu_kernel, dim3(grid_for(S * (I / 8))), dim3(256), 0, as_stream(stream), (const u32x4*)gu,
+                     S, I / 8, (u32x4*)act);
+  return launch_status("swiglu");
+}
+
+extern "C" int mlora_swiglu_backward(const void* gu, const void* dact, int64_t S, int64_t I, void* dgu, void* stream) {
+  clear_error();
+  if (I % 8) return fail("swiglu_backward: I=%lld must be a multiple of 8", (long long)I);
+  if (S == 0) return 0;
+  hipLaunchKernelGGL(swiglu_backward_kernel, dim3(grid_for(S * (I / 8))), dim3(256), 0, as_stream(stream),
+                     (const u32x4*)gu, (const u32x4*)dact, S, I / 8, (u32x4*)dgu);
+  return launch_status("swiglu_backward");
+}
+
+extern "C" int mlora_combine(const void* y, int64_t H, const void* w, int w_dtype, const int64_t* inv, int64_t T,
+                             int k, const int32_t* offsets, int E, void* out, void* stream) {
+  clear_error();
+  if (H % 8) return fail("combine: H=%lld must be a multiple of 8", (long long)H);
+  if (k < 1 || E < 1) return fail("combine: k=%d, E=%d must be >= 1", k, E);
+  if (T == 0) return 0;
+  const dim3 g(grid_for(T * (H / 8))), b(256);
+  if (w_dtype == MLORA_DT_F32)
+    hipLaunchKernelGGL(combine_kernel<float>, g, b, 0, as_stream(stream), (const u32x4*)y, H / 8, (const float*)w,
+                       inv, T, k, offsets, E, (u32x4*)out);
+  else if (w_dtype == MLORA_DT_BF16)
+    hipLaunchKernelGGL(combine_kernel<bf16>, g, b, 0, as_stream(stream), (const u32x4*)y, H / 8, (const bf16*)w, inv,
+                       T, k, offsets, E, (u32x4*)out);
+  else
+    return fail("combine: weight dtype %d is not bf16/f32", w_dtype);
+  return launch_status("combine");
+}
+
+extern "C" int mlora_combine_backward(const void* dout, const void* y, int64_t H, const void* w, int w_dtype,
+                                      const int64_t* inv, int64_t T, int k, const int32_t* offsets, int E, void* dy,
+                                      void* dw, void* stream) {
+  clear_error();
+  if (H % 8) return fail("combine_backward: H=%lld must be a multiple of 8", (long long)H);
+  if (k < 1 || E < 1) return fail("combine_backward: k=%d, E=%d must be >= 1", k, E);
+  if (T == 0) return 0;
+  if (T > 0x7FFFFFFF) return fail("combine_backward: T=%lld too large", (long long)T);
+  const dim3 g((unsigned)T), b(256);
+  if (w_dtype == MLORA_DT_F32)
+    hipLaunchKernelGGL(combine_backward_kernel<float>, g, b, 0, as_stream(stream), (const u32x4*)dout,
+                       (const u32x4*)y, H / 8, (const float*)w, inv, T, k, offsets, E, (u32x4*)dy, (float*)dw);
+  else if (w_dtype == MLORA_DT_BF16)
+    hipLaunchKernelGGL(combine_backward_kernel<bf16>, g, b, 0, as_stream(stream), (const u32x4*)dout,
+                       (const u32x4*)y, H / 8, (const bf16*)w, inv, T, k, offsets, E, (u32x4*)dy, (bf16*)dw);
+  else
+    return fail("combine_backward: weight dtype %d is not bf16/f32", w_dtype);
+  return launch_status("combine_backward");
+}

@@ -1,0 +1,604 @@
+// The grouped product of the experts with the rank-r LoRA fused in, for gfx950 (CDNA4) MFMA.
+//
+//   out_e = c · x_e W_e + scaling · bf16(x_e A_e) B_e + bias_e         for every expert e
+//
+// x's rows are sorted by expert; offsets[e] is the end of expert e's rows.  Each expert's rows are
+// cut into BM-row tiles (no tile spans two experts) and a work item is one (tile, BN-column block).
+// The kernel is persistent: the grid is a fixed number of workgroups per compute unit and each
+// workgroup derives the tile map itself, from offsets, in LDS (no tile arrays, no host round
+// trip).  Items are split into 8 contiguous ranges, one per XCD (the hardware deals workgroup b to
+// XCD b % 8), so that the workgroups running together on one XCD work on neighbouring tiles of
+// the same expert and share its weight tiles and x tiles in that XCD's L2.
+//
+// Main loop: BK-deep stages double-buffered in LDS.  x tiles (BM x BK) and weight tiles (BN x BK)
+// are held in LDS as [row][k] bf16 with k contiguous, whatever the stack's layout:
+//   * a stack whose k axis is contiguous is copied 8 k-values at a time;
+//   * a stack whose n axis is contiguous (the input-gradient pass of an (E, out, in) stack) is
+//     loaded as 4(k) x 8(n) blocks and transposed in registers (v_perm_b32) on the way to LDS;
+//   * fp8 e4m3 and NF4 stacks are decoded to bf16 in registers between the global load and the
+//     LDS store, with a per-output-row scale folded in when it runs along k.
+// Global loads go through buffer resources (32-bit offsets; reads past a resource's end return
+// zero), which bounds every tile at the end of x and of each expert's weights.
+// Each of the 4 waves owns a 64 x 64 corner of the 128 x 128 tile: 2 x 2 v_mfma_f32_32x32x16_bf16
+// accumulators.  The LoRA's x·A_e (BM x R, R a multiple of 16) is accumulated in the same loop
+// from the same LDS x tile with v_mfma_f32_16x16x32_bf16, each wave taking 32 of the rows, so x is
+// read from HBM once for both products.  The epilogue rounds x·A_e to bf16 (as the reference
+// does), optionally stores it ("low", kept for the backward pass), and adds scaling · low · B_e
+// with one more MFMA of depth R, then the scale and the bias.
+//
+// Reference behaviour: src/meepsquared/_grouped.py:120-221 (_grouped_gemm_kernel), :313-345 (_launch).
+#include <mutex>
+#include <unordered_map>
+
+#include "common.hpp"
+
+namespace mlora {
+
+constexpr int BM = 128, BN = 128, BK = 64;
+constexpr int BKP = BK + 8;  // LDS row pitch in bf16: rows 144 bytes apart keep ds_read_b128 free of conflicts
+constexpr int kThreads = 256;
+constexpr int WAVES_N = 2;
+constexpr int WTM = 64, WTN = 64;   // each wave's corner
+constexpr int FM = WTM / 32, FN = WTN / 32;
+constexpr int kMaxRank = 64;
+constexpr int kXcds = 8;
+constexpr uint32_t kOob = 0x80000000u;  // an offset past every resource's end: the load returns zero
+
+enum { W_BF16 = 0, W_FP8 = 1, W_NF4 = 2 };
+
+struct GemmArgs {
+  const bf16* x;
+  int64_t ldx;
+  const uint8_t* w;      // bytes
+  int64_t w_se, w_sk, w_sn;  // elements
+  const float* scale;
+  int64_t scale_se;
+  int scale_kind;
+  const uint8_t* nf4_q;
+  const float* nf4_absmax2;
+  const float* nf4_code2;
+  const float* nf4_offset;
+  const float* nf4_code;
+  const bf16* at;        // A_e^T: [e][r][k], k contiguous
+  int64_t at_se, at_sr;
+  const bf16* bt;        // B_e^T: [e][n][r], r contiguous
+  int64_t bt_se, bt_sn;
+  int rank;              // a multiple of 16
+  float scaling;
+  const bf16* bias;
+  int64_t bias_se;
+  bf16* out;
+  int64_t ldo;
+  bf16* low;
+  int64_t ldl;
+  const int32_t* offsets;
+  int64_t rows;
+  int E, K, N;
+};
+
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, int64_t bytes) {
+  const int64_t cap = 0x7FFFFFF0;
+  return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, (int)(bytes < cap ? bytes : cap), 0x00020000);
+}
+__device__ __forceinline__ u32x4 ld128(rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+__device__ __forceinline__ u32x2 ld64(rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
+}
+__device__ __forceinline__ uint32_t ld32(rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0); }
+
+__device__ __forceinline__ uint32_t lo_pair(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x05040100u); }
+__device__ __forceinline__ uint32_t hi_pair(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x07060302u); }
+
+// 8 fp8 (element 0 in the lowest byte) -> 8 bf16, each times s (exact when s == 1)
+__device__ __forceinline__ u32x4 fp8x8_to_bf16(u32x2 v, float s) {
+  u32x4 r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t d = v[i >> 1] >> (16 * (i & 1));
+    r[i] = pack_bf16x2(fp8_e4m3_to_f32(d & 0xFFu) * s, fp8_e4m3_to_f32((d >> 8) & 0xFFu) * s);
+  }
+  return r;
+}
+__device__ __forceinline__ u32x4 fp8x8_to_bf16_scaled(u32x2 v, const float* s) {
+  u32x4 r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t d = v[i >> 1] >> (16 * (i & 1));
+    r[i] = pack_bf16x2(fp8_e4m3_to_f32(d & 0xFFu) * s[2 * i], fp8_e4m3_to_f32((d >> 8) & 0xFFu) * s[2 * i + 1]);
+  }
+  return r;
+}
+// 8 NF4 codes in 4 bytes (byte j: element 2j in the high nibble, 2j+1 in the low) -> 8 bf16 · absmax
+__device__ __forceinline__ u32x4 nf4x8_to_bf16(uint32_t v, float absmax, const float* code) {
+  u32x4 r;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t byte = (v >> (8 * j)) & 0xFFu;
+    r[j] = pack_bf16x2(code[byte >> 4] * absmax, code[byte & 0xFu] * absmax);
+  }
+  return r;
+}
+__device__ __forceinline__ float nf4_block_absmax(const GemmArgs& p, int64_t block) {
+  return p.nf4_code2[p.nf4_q[block]] * p.nf4_absmax2[block >> 8] + p.nf4_offset[0];
+}
+
+// Byte offset of a stack element (NF4: two per byte).
+template <int WDT>
+__device__ __forceinline__ uint32_t w_bytes(int64_t el) {
+  if constexpr (WDT == W_BF16) return (uint32_t)(el * 2);
+  else if constexpr (WDT == W_FP8) return (uint32_t)el;
+  else return (uint32_t)(el >> 1);
+}
+
+// One BK-deep stage: the global loads land in registers (issued a stage ahead) and are decoded
+// into LDS after the current stage's MFMAs.
+template <int WDT, bool BKC, bool SCALE_K, int NRB>
+struct Stage {
+  static constexpr int kAChunks = NRB * 16 * BK / 8;  // 16-byte chunks of A^T per stage
+  static constexpr int kAPer = (kAChunks + kThreads - 1) / kThreads;
+  u32x4 x[4];
+  u32x4 w16[4];
+  u32x2 w8[4];
+  uint32_t w4[4];
+  float ws[BKC && SCALE_K ? 32 : 4];
+  u32x4 a[kAPer > 0 ? kAPer : 1];
+
+  __device__ __forceinline__ void load(const GemmArgs& p, rsrc_t rx, rsrc_t rw, rsrc_t ra, int e, int n0, int k0,
+                                       int tid) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = tid + i * kThreads;
+      const int rr = c >> 3, k = k0 + (c & 7) * 8;
+      x[i] = ld128(rx, k < p.K ? (uint32_t)((rr * p.ldx + k) * 2) : kOob);
+    }
+    if constexpr (BKC) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int c = tid + i * kThreads;
+        const int n = n0 + (c >> 3), k = k0 + (c & 7) * 8;
+        const bool ok = n < p.N && k < p.K;
+        const int64_t el = (int64_t)n * p.w_sn + k;
+        const uint32_t off = ok ? w_bytes<WDT>(el) : kOob;
+        if constexpr (WDT == W_BF16) {
+          w16[i] = ld128(rw, off);
+        } else if constexpr (WDT == W_FP8) {
+          w8[i] = ld64(rw, off);
+          if constexpr (SCALE_K) {
+#pragma unroll
+            for (int q = 0; q < 8; ++q) ws[i * 8 + q] = ok ? p.scale[(int64_t)e * p.scale_se + k + q] : 0.f;
+          }
+        } else {
+          w4[i] = ld32(rw, off);
+          ws[i] = ok ? nf4_block_absmax(p, ((int64_t)e * p.w_se + el) >> 6) : 0.f;
+        }
+      }
+    } else {
+      const int kb = tid & 15, n = n0 + (tid >> 4) * 8;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int k = k0 + kb * 4 + q;
+        const bool ok = n < p.N && k < p.K;
+        const int64_t el = (int64_t)k * p.w_sk + n;
+        const uint32_t off = ok ? w_bytes<WDT>(el) : kOob;
+        if constexpr (WDT == W_BF16) {
+          w16[q] = ld128(rw, off);
+        } else if constexpr (WDT == W_FP8) {
+          w8[q] = ld64(rw, off);
+          if constexpr (SCALE_K) ws[q] = ok ? p.scale[(int64_t)e * p.scale_se + k] : 0.f;
+        } else {
+          w4[q] = ld32(rw, off);
+          ws[q] = ok ? nf4_block_absmax(p, ((int64_t)e * p.w_se + el) >> 6) : 0.f;
+        }
+      }
+    }
+    if constexpr (NRB > 0) {
+#pragma unroll
+      for (int i = 0; i < kAPer; ++i) {
+        const int c = tid + i * kThreads;
+        const int r = c >> 3, k = k0 + (c & 7) * 8;
+        if (c < kAChunks) a[i] = ld128(ra, k < p.K ? (uint32_t)((r * p.at_sr + k) * 2) : kOob);
+      }
+    }
+  }
+
+  __device__ __forceinline__ void store(bf16* As, bf16* Bs, bf16* Aa, const float* code, int tid) const {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = tid + i * kThreads;
+      *(u32x4*)(As + (c >> 3) * BKP + (c & 7) * 8) = x[i];
+    }
+    if constexpr (BKC) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int c = tid + i * kThreads;
+        u32x4 v;
+        if constexpr (WDT == W_BF16) v = w16[i];
+        else if constexpr (WDT == W_FP8) v = SCALE_K ? fp8x8_to_bf16_scaled(w8[i], ws + i * 8) : fp8x8_to_bf16(w8[i], 1.0f);
+        else v = nf4x8_to_bf16(w4[i], ws[i], code);
+        *(u32x4*)(Bs + (c >> 3) * BKP + (c & 7) * 8) = v;
+      }
+    } else {
+      const int kb = tid & 15, nb8 = tid >> 4;
+      u32x4 row[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        if constexpr (WDT == W_BF16) row[q] = w16[q];
+        else if constexpr (WDT == W_FP8) row[q] = fp8x8_to_bf16(w8[q], SCALE_K ? ws[q] : 1.0f);
+        else row[q] = nf4x8_to_bf16(w4[q], ws[q], code);
+      }
+      // transpose 4 (k) x 8 (n) into 8 rows (n) of 4 k
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        u32x2 ev, od;
+        ev[0] = lo_pair(row[0][m], row[1][m]);
+        ev[1] = lo_pair(row[2][m], row[3][m]);
+        od[0] = hi_pair(row[0][m], row[1][m]);
+        od[1] = hi_pair(row[2][m], row[3][m]);
+        *(u32x2*)(Bs + (nb8 * 8 + 2 * m) * BKP + kb * 4) = ev;
+        *(u32x2*)(Bs + (nb8 * 8 + 2 * m + 1) * BKP + kb * 4) = od;
+      }
+    }
+    if constexpr (NRB > 0) {
+#pragma unroll
+      for (int i = 0; i < kAPer; ++i) {
+        const int c = tid + i * kThreads;
+        if (c < kAChunks) *(u32x4*)(Aa + (c >> 3) * BKP + (c & 7) * 8) = a[i];
+      }
+    }
+  }
+};
+
+// NRB = rank / 16 (0: no adapters).
+template <int WDT, bool BKC, bool SCALE_K, int NRB>
+__global__ __launch_bounds__(kThreads, 2) void grouped_gemm_kernel(GemmArgs p) {
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  constexpr int RP = NRB * 16;
+  constexpr int LP = RP + 8;  // pitch of the epilogue's low and B^T tiles
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+  const int E = p.E;
+
+  bf16* As = (bf16*)smem;                    // [2][BM][BKP]
+  bf16* Bs = As + 2 * BM * BKP;              // [2][BN][BKP]
+  bf16* Aa = Bs + 2 * BN * BKP;              // [2][RP][BKP]
+  int* starts = (int*)(Aa + 2 * RP * BKP);   // E + 1
+  int* tstart = starts + (E + 1);            // E + 1
+  float* code = (float*)(tstart + (E + 1));  // 16 (NF4 code book)
+  bf16* Ls = As;                             // epilogue: [BM][LP], aliasing the x stages
+  bf16* Lb = As + BM * LP;                   // epilogue: [BN][LP]
+
+  // ---- the tile map, from offsets ----
+  // row starts clamped into [0, rows]: offsets past the end of x (a caller's mistake) cannot send a
+  // tile outside x or out
+  for (int e = tid; e <= E; e += kThreads) {
+    const int64_t o = e == 0 ? 0 : (int64_t)p.offsets[e - 1];
+    starts[e] = (int)(o < 0 ? 0 : (o > p.rows ? p.rows : o));
+  }
+  if constexpr (WDT == W_NF4) {
+    if (tid < 16) code[tid] = p.nf4_code[tid];
+  }
+  __syncthreads();
+  for (int e = tid; e < E; e += kThreads) tstart[e] = max(starts[e + 1] - starts[e], 0) / BM + ((max(starts[e + 1] - starts[e], 0) % BM) != 0);
+  __syncthreads();
+  if (wave == 0) {  // exclusive scan of tstart[0..E), 64 at a time
+    int run = 0;
+    for (int base = 0; base < E; base += 64) {
+      const int e = base + lane;
+      const int v = e < E ? tstart[e] : 0;
+      int incl = v;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int u = __shfl_up(incl, o, 64);
+        if (lane >= o) incl += u;
+      }
+      if (e < E) tstart[e] = run + incl - v;
+      run += __shfl(incl, 63, 64);
+    }
+    if (lane == 0) tstart[E] = run;
+  }
+  __syncthreads();
+  const int nb = (p.N + BN - 1) / BN;
+  const int64_t total = (int64_t)tstart[E] * nb;
+  const int xcd = blockIdx.x % kXcds, slot = blockIdx.x / kXcds, per_xcd = gridDim.x / kXcds;
+  const int64_t chunk = (total + kXcds - 1) / kXcds;
+  const int64_t beg = xcd * chunk, end = min(beg + chunk, total);
+  const int nk = (p.K + BK - 1) / BK;
+
+  for (int64_t item = beg + slot; item < end; item += per_xcd) {
+    const int t = (int)(item / nb), nblk = (int)(item - (int64_t)t * nb);
+    int lo = 0, hi = E - 1;  // the expert e with tstart[e] <= t < tstart[e+1]
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (tstart[mid] <= t) lo = mid; else hi = mid - 1;
+    }
+    const int e = lo;
+    const int64_t row0 = (int64_t)starts[e] + (int64_t)(t - tstart[e]) * BM;
+    const int mrows = (int)min((int64_t)BM, (int64_t)starts[e + 1] - row0);
+    const int n0 = nblk * BN;
+
+    // resources: x from this tile's first row to at most BM rows on; W and A^T of expert e
+    const int64_t xrows = min((int64_t)BM, p.rows - row0);
+    const rsrc_t rx = make_rsrc(p.x + row0 * p.ldx, xrows * p.ldx * 2);
+    const int64_t we = (int64_t)e * p.w_se;
+    const rsrc_t rw = WDT == W_BF16 ? make_rsrc(p.w + we * 2, p.w_se * 2)
+                    : WDT == W_FP8  ? make_rsrc(p.w + we, p.w_se)
+                                    : make_rsrc(p.w + (we >> 1), p.w_se >> 1);
+    rsrc_t ra = rx;
+    if constexpr (NRB > 0) ra = make_rsrc(p.at + (int64_t)e * p.at_se, (int64_t)RP * p.at_sr * 2);
+
+    f32x16 acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j) acc[i][j] = f32x16{};
+    f32x4 lacc[2][NRB > 0 ? NRB : 1];
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int j = 0; j < (NRB > 0 ? NRB : 1); ++j) lacc[h][j] = f32x4{};
+
+    Stage<WDT, BKC, SCALE_K, NRB> st;
+    __syncthreads();  // the previous item's epilogue is done with the LDS
+    st.load(p, rx, rw, ra, e, n0, 0, tid);
+    st.store(As, Bs, Aa, code, tid);
+    __syncthreads();
+
+    for (int kt = 0; kt < nk; ++kt) {
+      const int buf = kt & 1;
+      if (kt + 1 < nk) st.load(p, rx, rw, ra, e, n0, (kt + 1) * BK, tid);
+      const bf16* as = As + buf * BM * BKP;
+      const bf16* bs = Bs + buf * BN * BKP;
+#pragma unroll
+      for (int kk = 0; kk < BK / 16; ++kk) {
+        bf16x8 af[FM], bfr[FN];
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+          af[i] = *(const bf16x8*)(as + (wm * WTM + i * 32 + (lane & 31)) * BKP + kk * 16 + (lane >> 5) * 8);
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+          bfr[j] = *(const bf16x8*)(bs + (wn * WTN + j * 32 + (lane & 31)) * BKP + kk * 16 + (lane >> 5) * 8);
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+          for (int j = 0; j < FN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+      }
+      if constexpr (NRB > 0) {
+        const bf16* aa = Aa + buf * RP * BKP;
+        const int lr0 = wm * WTM + wn * 32;  // this wave's 32 rows of x·A_e
+#pragma unroll
+        for (int kk = 0; kk < BK / 32; ++kk) {
+          bf16x8 xf[2];
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+            xf[h] = *(const bf16x8*)(as + (lr0 + h * 16 + (lane & 15)) * BKP + kk * 32 + (lane >> 4) * 8);
+#pragma unroll
+          for (int rb = 0; rb < NRB; ++rb) {
+            const bf16x8 af = *(const bf16x8*)(aa + (rb * 16 + (lane & 15)) * BKP + kk * 32 + (lane >> 4) * 8);
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+              lacc[h][rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf[h], af, lacc[h][rb], 0, 0, 0);
+          }
+        }
+      }
+      if (kt + 1 < nk)
+        st.store(As + (buf ^ 1) * BM * BKP, Bs + (buf ^ 1) * BN * BKP, Aa + (buf ^ 1) * RP * BKP, code, tid);
+      __syncthreads();
+    }
+
+    // ---- epilogue ----
+    float cscale[FN];
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      float c = 1.0f;
+      if (p.scale_kind == MLORA_SCALE_EXPERT) c = p.scale[e];
+      else if (p.scale_kind == MLORA_SCALE_ROW && !SCALE_K) {
+        const int n = n0 + wn * WTN + j * 32 + (lane & 31);
+        c = n < p.N ? p.scale[(int64_t)e * p.scale_se + n] : 0.f;
+      }
+      cscale[j] = c;
+    }
+    if constexpr (NRB > 0) {
+      const int lr0 = wm * WTM + wn * 32;
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int rb = 0; rb < NRB; ++rb)
+#pragma unroll
+          for (int v = 0; v < 4; ++v)
+            Ls[(lr0 + h * 16 + 4 * (lane >> 4) + v) * LP + rb * 16 + (lane & 15)] = (bf16)lacc[h][rb][v];
+      // B_e^T rows n0 .. n0+BN: Lb[n][r]
+      const rsrc_t rbt = make_rsrc(p.bt + (int64_t)e * p.bt_se, (int64_t)p.N * p.bt_sn * 2);
+      for (int c = tid; c < BN * RP / 8; c += kThreads) {
+        const int nn = c / (RP / 8), rc = (c - nn * (RP / 8)) * 8;
+        const int n = n0 + nn;
+        *(u32x4*)(Lb + nn * LP + rc) = ld128(rbt, n < p.N ? (uint32_t)((n * p.bt_sn + rc) * 2) : kOob);
+      }
+      __syncthreads();
+      if (p.low != nullptr && nblk == 0) {  // bf16(x·A_e) of the tile's rows, 16 bytes at a time
+        for (int c = tid; c < BM * RP / 8; c += kThreads) {
+          const int m = c / (RP / 8), rc = (c - m * (RP / 8)) * 8;
+          if (m < mrows) *(u32x4*)(p.low + (row0 + m) * p.ldl + rc) = *(const u32x4*)(Ls + m * LP + rc);
+        }
+      }
+      if (p.scaling != 0.f) {
+        // out = s · (c/s · x W + low B): the low-rank product joins the accumulator through one MFMA
+        const float inv_s = 1.0f / p.scaling;
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+          for (int j = 0; j < FN; ++j) acc[i][j] *= cscale[j] * inv_s;
+#pragma unroll
+        for (int rk = 0; rk < NRB; ++rk) {
+          bf16x8 lf[FM], bfr[FN];
+#pragma unroll
+          for (int i = 0; i < FM; ++i)
+            lf[i] = *(const bf16x8*)(Ls + (wm * WTM + i * 32 + (lane & 31)) * LP + rk * 16 + (lane >> 5) * 8);
+#pragma unroll
+          for (int j = 0; j < FN; ++j)
+            bfr[j] = *(const bf16x8*)(Lb + (wn * WTN + j * 32 + (lane & 31)) * LP + rk * 16 + (lane >> 5) * 8);
+#pragma unroll
+          for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+              acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(lf[i], bfr[j], acc[i][j], 0, 0, 0);
+        }
+#pragma unroll
+        for (int j = 0; j < FN; ++j) cscale[j] = p.scaling;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const int n = n0 + wn * WTN + j * 32 + (lane & 31);
+      if (n >= p.N) continue;
+      const float bias = p.bias != nullptr ? (float)p.bias[(int64_t)e * p.bias_se + n] : 0.f;
+      bf16* o = p.out + row0 * p.ldo + n;
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int row = wm * WTM + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+          if (row < mrows) o[row * p.ldo] = (bf16)(acc[i][j][v] * cscale[j] + bias);
+        }
+    }
+  }
+}
+
+// ---- launch ----
+static size_t lds_bytes(int rp, int E) {
+  return (size_t)2 * (BM + BN + rp) * BKP * sizeof(bf16) + (size_t)(2 * (E + 1) + 16) * sizeof(int);
+}
+static_assert(BM * (kMaxRank + 8) + BN * (kMaxRank + 8) <= 2 * BM * BKP, "epilogue views overflow the x stages");
+
+template <int WDT, bool BKC, bool SCALE_K, int NRB>
+static int launch_t(const GemmArgs& a, hipStream_t s) {
+  auto kern = grouped_gemm_kernel<WDT, BKC, SCALE_K, NRB>;
+  const size_t lds = lds_bytes(NRB * 16, a.E);
+  static std::mutex mu;
+  static std::unordered_map<int64_t, int> grid_cache;  // (device, lds) -> grid
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return fail("grouped_gemm: hipGetDevice failed");
+  int grid = 0;
+  {
+    std::lock_guard<std::mutex> g(mu);
+    const int64_t key = ((int64_t)dev << 32) | (int64_t)lds;
+    auto it = grid_cache.find(key);
+    if (it != grid_cache.end()) {
+      grid = it->second;
+    } else {
+      if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+        return fail("grouped_gemm: cannot grant %zu bytes of LDS", lds);
+      int cus = 0, per_cu = 0;
+      if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
+        return fail("grouped_gemm: cannot read the compute unit count");
+      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void*)kern, kThreads, lds) != hipSuccess ||
+          per_cu < 1)
+        per_cu = 1;
+      grid = (cus * per_cu + kXcds - 1) / kXcds * kXcds;
+      grid_cache[key] = grid;
+    }
+  }
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(kThreads), lds, s, a);
+  return launch_status("grouped_gemm");
+}
+
+template <int WDT, bool BKC, bool SCALE_K>
+static int launch_r(const GemmArgs& a, hipStream_t s) {
+  switch (a.rank / 16) {
+    case 0: return launch_t<WDT, BKC, SCALE_K, 0>(a, s);
+    case 1: return launch_t<WDT, BKC, SCALE_K, 1>(a, s);
+    case 2: return launch_t<WDT, BKC, SCALE_K, 2>(a, s);
+    case 3: return launch_t<WDT, BKC, SCALE_K, 3>(a, s);
+    default: return launch_t<WDT, BKC, SCALE_K, 4>(a, s);
+  }
+}
+
+}  // namespace mlora
+
+using namespace mlora;
+
+static bool aligned(const void* p, uintptr_t n) { return ((uintptr_t)p & (n - 1)) == 0; }
+
+extern "C" int mlora_grouped_gemm(const void* x, int64_t ldx, int64_t rows, int K, int N, const void* w, int w_dtype,
+                                  int64_t w_se, int64_t w_sk, int64_t w_sn, const float* scale, int scale_kind,
+                                  int64_t scale_se, int scale_on_k, const uint8_t* nf4_absmax_q,
+                                  const float* nf4_absmax2, const float* nf4_code2, const float* nf4_offset,
+                                  const float* nf4_code, const void* at, int64_t at_se, int64_t at_sr,
+                                  const void* bt, int64_t bt_se, int64_t bt_sn, int rank, float scaling,
+                                  const void* bias, int64_t bias_se, void* out, int64_t ldo, void* low, int64_t ldl,
+                                  const int32_t* offsets, int E, void* stream) {
+  clear_error();
+  if (rows < 0) return fail("grouped_gemm: rows=%lld is negative", (long long)rows);
+  if (E < 1 || E > 4096) return fail("grouped_gemm: E=%d outside [1, 4096]", E);
+  if (K < 8 || K % 8) return fail("grouped_gemm: K=%d must be a positive multiple of 8", K);
+  if (N < 8 || N % 8) return fail("grouped_gemm: N=%d must be a positive multiple of 8", N);
+  if (ldx < K || ldx % 8 || !aligned(x, 16))
+    return fail("grouped_gemm: x needs a 16-byte aligned base and a row stride (%lld) that is a multiple of 8 and >= K",
+                (long long)ldx);
+  if (ldo < N) return fail("grouped_gemm: ldo=%lld < N=%d", (long long)ldo, N);
+  if ((int64_t)BM * ldx * 2 > 0x7FFFFFF0) return fail("grouped_gemm: row stride %lld too large", (long long)ldx);
+  const bool bkc = w_sk == 1;
+  if (!bkc && w_sn != 1)
+    return fail("grouped_gemm: the stack needs a unit stride along k or n (w_sk=%lld, w_sn=%lld)", (long long)w_sk,
+                (long long)w_sn);
+  const int64_t other = bkc ? w_sn : w_sk;
+  const int64_t esize = w_dtype == MLORA_DT_BF16 ? 2 : 1;
+  if (w_se * esize > 0x7FFFFFF0) return fail("grouped_gemm: one expert's weights exceed 2 GiB");
+  if (w_dtype == MLORA_DT_BF16) {
+    if (other % 8 || w_se % 8 || !aligned(w, 16)) return fail("grouped_gemm: a bf16 stack needs 16-byte aligned rows");
+  } else if (w_dtype == MLORA_DT_FP8_E4M3) {
+    if (other % 8 || w_se % 8 || !aligned(w, 8)) return fail("grouped_gemm: an fp8 stack needs 8-byte aligned rows");
+  } else if (w_dtype == MLORA_DT_NF4) {
+    if (other % 64 || w_se % 64 || !aligned(w, 4))
+      return fail("grouped_gemm: an NF4 stack needs rows of a multiple of 64 values");
+    if (!nf4_absmax_q || !nf4_absmax2 || !nf4_code2 || !nf4_offset || !nf4_code)
+      return fail("grouped_gemm: an NF4 stack needs its absmax_q, absmax2, code2, offset and code");
+  } else {
+    return fail("grouped_gemm: stack dtype %d is not bf16, fp8 e4m3 or NF4", w_dtype);
+  }
+  if (scale_kind < 0 || scale_kind > 2) return fail("grouped_gemm: scale_kind %d unknown", scale_kind);
+  if (scale_kind != MLORA_SCALE_NONE && scale == nullptr)
+    return fail("grouped_gemm: scale_kind %d without a scale", scale_kind);
+  const bool scale_k = scale_kind == MLORA_SCALE_ROW && scale_on_k;
+  if (scale_k && w_dtype != MLORA_DT_FP8_E4M3) return fail("grouped_gemm: a per-row scale along k is for fp8 stacks");
+  const bool lora = at != nullptr;
+  if (lora) {
+    if (bt == nullptr) return fail("grouped_gemm: adapter A without B");
+    if (rank < 16 || rank > kMaxRank || rank % 16)
+      return fail("grouped_gemm: rank=%d must be 16, 32, 48 or 64 (pad with zeros)", rank);
+    if (at_sr < K || at_sr % 8 || at_se % 8 || !aligned(at, 16))
+      return fail("grouped_gemm: A^T needs 16-byte aligned rows of >= K values");
+    if (bt_sn < rank || bt_sn % 8 || bt_se % 8 || !aligned(bt, 16))
+      return fail("grouped_gemm: B^T needs 16-byte aligned rows of >= rank values");
+    if (low != nullptr && (ldl < rank || ldl % 8 || !aligned(low, 16)))
+      return fail("grouped_gemm: low needs 16-byte aligned rows of >= rank values");
+  }
+  if (rows == 0) return 0;
+
+  GemmArgs g;
+  g.x = (const bf16*)x; g.ldx = ldx;
+  g.w = (const uint8_t*)w; g.w_se = w_se; g.w_sk = w_sk; g.w_sn = w_sn;
+  g.scale = scale; g.scale_se = scale_se; g.scale_kind = scale_kind;
+  g.nf4_q = nf4_absmax_q; g.nf4_absmax2 = nf4_absmax2; g.nf4_code2 = nf4_code2; g.nf4_offset = nf4_offset;
+  g.nf4_code = nf4_code;
+  g.at = (const bf16*)at; g.at_se = at_se; g.at_sr = at_sr;
+  g.bt = (const bf16*)bt; g.bt_se = bt_se; g.bt_sn = bt_sn;
+  g.rank = lora ? rank : 0;
+  g.scaling = scaling;
+  g.bias = (const bf16*)bias; g.bias_se = bias_se;
+  g.out = (bf16*)out; g.ldo = ldo;
+  g.low = lora ? (bf16*)low : nullptr; g.ldl = ldl;
+  g.offsets = offsets; g.rows = rows; g.E = E; g.K = K; g.N = N;
+  hipStream_t s = as_stream(stream);
+  switch (w_dtype) {
+    case MLORA_DT_BF16: return bkc ? launch_r<W_BF16, true, false>(g, s) : launch_r<W_BF16, false, false>(g, s);
+    case MLORA_DT_FP8_E4M3:
+      if (scale_k) return bkc ? launch_r<W_FP8, true, true>(g, s) : launch_r<W_FP8, false, true>(g, s);
+      return bkc ? launch_r<W_FP8, true, false>(g, s) : launch_r<W_FP8, false, false>(g, s);
+    default: return bkc ? launch_r<W_NF4, true, false>(g, s) : launch_r<W_NF4, false, false>(g, s);
+  }
+}

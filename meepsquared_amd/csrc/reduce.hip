@@ -1,0 +1,124 @@
+// The adapters' gradients: for every expert e,
+//
+//   out[e, n, r] = bf16(scaling · sum over expert e's rows of g[row, n] · l[row, r])
+//
+// a product whose depth is the expert's row count.  One workgroup per (expert, 64 columns of g)
+// walks the expert's rows 64 at a time: a 64-row slice of g is transposed into LDS as [n][row]
+// (k = rows contiguous, the MFMA's layout) and the matching slice of l as [r][row]; each wave
+// accumulates a 16 x R block with v_mfma_f32_16x16x32_bf16 in fp32.  The next slice is loaded into
+// registers while the current one is multiplied.  Every output element has exactly one writer
+// and a fixed summation order: no atomics, the same bits every run.
+//
+// Reference behaviour: src/meepsquared/_grouped.py:232-256 (_grouped_reduce_kernel), :362-370 (_reduce).
+#include "common.hpp"
+
+namespace mlora {
+
+constexpr int RB_N = 64;     // columns of g per workgroup
+constexpr int RB_ROWS = 64;  // rows per slice
+constexpr int RP_ = RB_ROWS + 8;
+
+__device__ __forceinline__ uint32_t lo2(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x05040100u); }
+__device__ __forceinline__ uint32_t hi2(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x07060302u); }
+
+template <int NRB>
+__global__ __launch_bounds__(256) void grouped_reduce_kernel(const bf16* __restrict__ g, int64_t ldg,
+                                                             const bf16* __restrict__ l, int64_t ldl, int64_t rows,
+                                                             int N, float scaling, const int32_t* __restrict__ offsets,
+                                                             bf16* __restrict__ out, int64_t o_se, int64_t o_sn,
+                                                             int64_t o_sr) {
+  constexpr int R = NRB * 16;
+  __shared__ __attribute__((aligned(16))) bf16 Gs[RB_N * RP_];  // [n][row]
+  __shared__ __attribute__((aligned(16))) bf16 Ls[R * RP_];     // [r][row]
+  const int e = blockIdx.x, n0 = blockIdx.y * RB_N;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // the expert's rows, clamped into [0, rows]
+  const int64_t start = e == 0 ? 0 : min(max((int64_t)offsets[e - 1], (int64_t)0), rows);
+  const int64_t end = min(max((int64_t)offsets[e], (int64_t)0), rows);
+
+  // this thread's 2 rows x 8 columns of g, and (threads < 32 * R/8) 2 rows x 8 ranks of l
+  const int gr = (tid >> 3) * 2, gc = (tid & 7) * 8;
+  const int lr = (tid / (R / 8)) * 2, lc = (tid % (R / 8)) * 8;
+  const bool l_owner = tid < 32 * (R / 8);
+  const bool g_cols = n0 + gc < N;
+
+  u32x4 gv[2], lv[2];
+  auto load = [&](int64_t row0) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int64_t row = row0 + gr + q;
+      gv[q] = (row < end && g_cols) ? *(const u32x4*)(g + row * ldg + n0 + gc) : u32x4{0u, 0u, 0u, 0u};
+      const int64_t lrow = row0 + lr + q;
+      if (l_owner) lv[q] = lrow < end ? *(const u32x4*)(l + lrow * ldl + lc) : u32x4{0u, 0u, 0u, 0u};
+    }
+  };
+  auto store = [&]() {
+    // transpose 2 rows x 8 columns into 8 columns x 2 rows
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      *(uint32_t*)(Gs + (gc + 2 * m) * RP_ + gr) = lo2(gv[0][m], gv[1][m]);
+      *(uint32_t*)(Gs + (gc + 2 * m + 1) * RP_ + gr) = hi2(gv[0][m], gv[1][m]);
+      if (l_owner) {
+        *(uint32_t*)(Ls + (lc + 2 * m) * RP_ + lr) = lo2(lv[0][m], lv[1][m]);
+        *(uint32_t*)(Ls + (lc + 2 * m + 1) * RP_ + lr) = hi2(lv[0][m], lv[1][m]);
+      }
+    }
+  };
+
+  f32x4 acc[NRB];
+#pragma unroll
+  for (int j = 0; j < NRB; ++j) acc[j] = f32x4{};
+  if (start < end) load(start);
+  for (int64_t row0 = start; row0 < end; row0 += RB_ROWS) {
+    store();
+    __syncthreads();
+    if (row0 + RB_ROWS < end) load(row0 + RB_ROWS);
+#pragma unroll
+    for (int kk = 0; kk < RB_ROWS / 32; ++kk) {
+      const bf16x8 a = *(const bf16x8*)(Gs + (wave * 16 + (lane & 15)) * RP_ + kk * 32 + (lane >> 4) * 8);
+#pragma unroll
+      for (int j = 0; j < NRB; ++j) {
+        const bf16x8 b = *(const bf16x8*)(Ls + (j * 16 + (lane & 15)) * RP_ + kk * 32 + (lane >> 4) * 8);
+        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc[j], 0, 0, 0);
+      }
+    }
+    __syncthreads();
+  }
+  // acc[j][v]: n = n0 + wave*16 + 4*(lane/16) + v, r = j*16 + lane%16
+#pragma unroll
+  for (int j = 0; j < NRB; ++j)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int n = n0 + wave * 16 + 4 * (lane >> 4) + v;
+      const int r = j * 16 + (lane & 15);
+      if (n < N) out[(int64_t)e * o_se + (int64_t)n * o_sn + (int64_t)r * o_sr] = (bf16)(acc[j][v] * scaling);
+    }
+}
+
+}  // namespace mlora
+
+using namespace mlora;
+
+extern "C" int mlora_grouped_reduce(const void* g, int64_t ldg, const void* l, int64_t ldl, int64_t rows, int N, int R,
+                                    float scaling, const int32_t* offsets, int E, void* out, int64_t o_se,
+                                    int64_t o_sn, int64_t o_sr, void* stream) {
+  clear_error();
+  if (E < 1 || E > 65535) return fail("grouped_reduce: E=%d outside [1, 65535]", E);
+  if (N < 8 || N % 8 || ldg < N || ldg % 8 || ((uintptr_t)g & 15u))
+    return fail("grouped_reduce: g needs N (%d) and its row stride (%lld) multiples of 8, 16-byte aligned", N, (long long)ldg);
+  if (R < 16 || R > 64 || R % 16) return fail("grouped_reduce: R=%d must be 16, 32, 48 or 64", R);
+  if (ldl < R || ldl % 8 || ((uintptr_t)l & 15u)) return fail("grouped_reduce: l needs 16-byte aligned rows of >= R values");
+  const dim3 grid((unsigned)E, (unsigned)((N + RB_N - 1) / RB_N)), block(256);
+  hipStream_t s = as_stream(stream);
+#define MLORA_RED(NRB)                                                                                               \
+  hipLaunchKernelGGL(grouped_reduce_kernel<NRB>, grid, block, 0, s, (const bf16*)g, ldg, (const bf16*)l, ldl, rows, \
+                     N, scaling, offsets, (bf16*)out, o_se, o_sn, o_sr)
+  switch (R / 16) {
+    case 1: MLORA_RED(1); break;
+    case 2: MLORA_RED(2); break;
+    case 3: MLORA_RED(3); break;
+    default: MLORA_RED(4); break;
+  }
+#undef MLORA_RED
+  return launch_status("grouped_reduce");
+}

@@ -1,0 +1,93 @@
+"""Stack-format oracle: fp8 e4m3 (per expert or per output row) and NF4 with double quantisation.
+
+TEST INFRASTRUCTURE ONLY (see oracle/__init__.py).
+"""
+
+import numpy as np
+import torch
+
+E4M3_MAX = 448.0
+
+
+def fp8_quantize(w, per_row=False, is_transposed=False):
+    """(q e4m3 tensor, scale fp32) — src/meepsquared/_fp8.py:122-128, scale = max(amax, 1e-12) / 448.
+
+    per_row: one scale per output row (dim 1 of (E, out, in), dim 2 of (E, in, out)).
+    Pinned by: torch's float8_e4m3fn cast (a library) and the round-trip bound of
+    tests/test_fp8.py:122-131 (error <= 0.07 · amax of the group).
+    """
+    w = torch.as_tensor(w).float()
+    if per_row:
+        amax = w.abs().amax(dim=1 if is_transposed else 2)
+        scale = torch.clamp(amax, min=1e-12) / E4M3_MAX
+        s = scale.unsqueeze(1) if is_transposed else scale.unsqueeze(2)
+    else:
+        amax = w.abs().flatten(1).amax(dim=1)
+        scale = torch.clamp(amax, min=1e-12) / E4M3_MAX
+        s = scale.view(-1, 1, 1)
+    return (w / s).to(torch.float8_e4m3fn), scale
+
+
+def fp8_dequantize(q, scale, is_transposed=False):
+    """q · scale in fp32 — src/meepsquared/_fp8.py:131-134 (per-row: broadcast along the row)."""
+    q = q.float()
+    if scale.dim() == 1:
+        return q * scale.view(-1, 1, 1)
+    return q * (scale.unsqueeze(1) if is_transposed else scale.unsqueeze(2))
+
+
+def nf4_code_from_definition():
+    """The 16 NF4 values from QLoRA's definition (Dettmers et al. 2023, Appendix E): 8 positive
+    quantiles of N(0,1) from the upper half (offset 0.9677 = 1/2 (1/(2·15) + 1/(2·16)) mapped to
+    the tail), 7 negative ones, an exact zero, normalised by the largest magnitude."""
+    from scipy.stats import norm
+
+    offset = 0.9677083
+    pos = norm.ppf(np.linspace(offset, 0.5, 9)[:-1]).tolist()
+    neg = (-norm.ppf(np.linspace(offset, 0.5, 8)[:-1])).tolist()
+    v = np.array(sorted(pos + [0.0] + neg))
+    return v / np.abs(v).max()
+
+
+def nearest_index(values, code):
+    """Index of the nearest code entry, ties to the lower index (numpy argmin's first minimum)."""
+    values = np.asarray(values, dtype=np.float32)[..., None]
+    d = np.abs(values - np.asarray(code, dtype=np.float32))
+    return d.argmin(axis=-1)
+
+
+def nf4_quantize(x, code, code2, blocksize=64, blocksize2=256):
+    """(packed uint8, absmax_q uint8, absmax2 fp32, offset fp32) of the flat values x.
+
+    The double-quant NF4 format of src/meepsquared/_vendor/axolotl/quantize.py:202-235's fields
+    (absmax per block, its 8-bit code with a second absmax and an offset): codes relative to each
+    block's exact absmax; the first value of a pair in the high nibble.
+    Pinned by: round-trip error bounds and code-boundary checks (tests/test_oracle.py); the
+    reference has no NF4 stack, so this format's bytes are this build's own.
+    """
+    x = np.asarray(x, dtype=np.float32).reshape(-1)
+    blocks = x.reshape(-1, blocksize)
+    absmax = np.abs(blocks).max(axis=1)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        inv = np.where(absmax > 0, np.float32(1.0) / absmax, np.float32(0.0)).astype(np.float32)
+    idx = nearest_index(blocks * inv[:, None], code).astype(np.uint8).reshape(-1)
+    packed = (idx[0::2] << 4) | idx[1::2]
+    offset = np.float32(absmax.astype(np.float64).mean())
+    centred = (absmax - offset).astype(np.float32)
+    pad = -centred.size % blocksize2
+    groups = np.concatenate([centred, np.zeros(pad, np.float32)]).reshape(-1, blocksize2)
+    absmax2 = np.abs(groups).max(axis=1).astype(np.float32)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        ratio = np.where(absmax2[:, None] > 0, groups / absmax2[:, None], 0).astype(np.float32)
+    absmax_q = nearest_index(ratio, code2).astype(np.uint8).reshape(-1)[: centred.size]
+    return packed.astype(np.uint8), absmax_q, absmax2, offset
+
+
+def nf4_dequantize(packed, absmax_q, absmax2, offset, code, code2, blocksize=64, blocksize2=256):
+    """code[nibble] · (code2[absmax_q[b]] · absmax2[b / 256] + offset), fp32."""
+    packed = np.asarray(packed, dtype=np.uint8)
+    nib = np.stack([packed >> 4, packed & 0xF], axis=1).reshape(-1)
+    b = np.arange(nib.size) // blocksize
+    code, code2 = np.asarray(code, np.float32), np.asarray(code2, np.float32)
+    absmax = (code2[np.asarray(absmax_q)[b]] * np.asarray(absmax2, np.float32)[b // blocksize2] + np.float32(offset)).astype(np.float32)
+    return (code[nib] * absmax).astype(np.float32)

@@ -1,0 +1,187 @@
+"""The grouped product kernel against the per-expert float32 oracle (mirrors the reference's
+tests/test_grouped.py), with the tolerances BASELINE states: relative Frobenius error <= 1e-2 for
+bf16 stacks, <= 3e-2 for fp8/NF4 stacks (against the oracle on the dequantised weights)."""
+
+import pytest
+import torch
+
+from helpers import offsets_of, rel
+from oracle import grouped as ref
+
+pytestmark = pytest.mark.gpu
+
+BF16_TOL = 1e-2
+Q_TOL = 3e-2
+
+
+@pytest.mark.parametrize("is_transposed", [False, True])
+@pytest.mark.parametrize("rows_per_expert,K,N", [
+    ([37, 0, 200, 64, 1], 96, 80),      # uneven groups, an empty one, sizes that are no multiples of the tiles
+    ([300] * 8, 256, 128),              # even groups
+    ([3], 2048, 1024),                  # one expert
+    ([130, 0, 0, 257, 0], 2048, 1536),  # tiles cut mid-expert, trailing empty experts
+])
+def test_the_kernel_matches_one_product_per_expert(is_transposed, rows_per_expert, K, N):
+    from meepsquared_amd import grouped_linear
+
+    torch.manual_seed(0)
+    rows, experts = sum(rows_per_expert), len(rows_per_expert)
+    x = torch.randn(rows, K, device="cuda", dtype=torch.bfloat16)
+    shape = (experts, K, N) if is_transposed else (experts, N, K)
+    weight = torch.randn(shape, device="cuda", dtype=torch.bfloat16) * 0.05
+    offsets = offsets_of(rows_per_expert)
+    out = grouped_linear(x, weight, offsets, is_transposed)
+    expected = ref.reference(x, weight, offsets.cpu(), is_transposed)
+    torch.testing.assert_close(out.float(), expected.float(), atol=2e-2, rtol=2e-2)
+    assert rel(out, ref.reference_lora(x, weight, None, offsets.cpu(), is_transposed, None, None, 1.0, out_dtype=torch.float32)) < BF16_TOL
+
+
+@pytest.mark.parametrize("is_transposed", [False, True])
+def test_the_kernel_takes_an_fp8_stack_as_weights_to_convert(is_transposed):
+    from meepsquared_amd import grouped_linear
+
+    torch.manual_seed(0)
+    x = torch.randn(70, 64, device="cuda", dtype=torch.bfloat16)
+    shape = (3, 64, 48) if is_transposed else (3, 48, 64)
+    weight = (torch.randn(shape, device="cuda") * 0.05).to(torch.float8_e4m3fn)
+    offsets = offsets_of([10, 40, 20])
+    out = grouped_linear(x, weight, offsets, is_transposed, products_fp8=False)
+    expected = ref.reference(x, weight.float(), offsets.cpu(), is_transposed)
+    torch.testing.assert_close(out.float(), expected.float(), atol=2e-2, rtol=2e-2)
+
+
+def test_rows_past_the_last_expert_are_left_alone():
+    from meepsquared_amd import grouped_linear
+
+    x = torch.randn(50, 64, device="cuda", dtype=torch.bfloat16)
+    weight = torch.randn(2, 32, 64, device="cuda", dtype=torch.bfloat16)
+    out = grouped_linear(x, weight, offsets_of([10, 20]), False)
+    assert out.shape == (50, 32)
+    expected = ref.reference(x[:30], weight, [10, 30], False)
+    torch.testing.assert_close(out[:30].float(), expected.float(), atol=2e-2, rtol=2e-2)
+
+
+def adapters(experts, K, N, rank, is_transposed):
+    if is_transposed:
+        lhs = torch.randn(experts, K, rank, device="cuda", dtype=torch.bfloat16) * 0.1
+        rhs = torch.randn(experts, rank, N, device="cuda", dtype=torch.bfloat16) * 0.1
+    else:
+        lhs = torch.randn(experts, N, rank, device="cuda", dtype=torch.bfloat16) * 0.1
+        rhs = torch.randn(experts, rank, K, device="cuda", dtype=torch.bfloat16) * 0.1
+    return lhs.requires_grad_(), rhs.requires_grad_()
+
+
+def run_both(x, weight, scale, offsets, is_transposed, lhs, rhs, scaling, bias, ref_weight=None, ref_scale="same"):
+    from meepsquared_amd import lora_linear
+
+    out = lora_linear(x, weight, scale, offsets, is_transposed, lhs, rhs, scaling, bias)
+    grad = torch.randn_like(out)
+    out.backward(grad)
+    got = (out.detach(), x.grad.clone(), lhs.grad.clone(), rhs.grad.clone())
+    x.grad = lhs.grad = rhs.grad = None
+    rw = weight if ref_weight is None else ref_weight
+    rs = scale if ref_scale == "same" else ref_scale
+    expected_out = ref.reference_lora(x, rw, rs, offsets.cpu(), is_transposed, lhs, rhs, scaling, bias, out_dtype=torch.float32)
+    expected_out.backward(grad.float())
+    expected = (expected_out.detach(), x.grad, lhs.grad, rhs.grad)
+    x.grad = lhs.grad = rhs.grad = None
+    return got, expected
+
+
+@pytest.mark.parametrize("is_transposed", [False, True])
+@pytest.mark.parametrize("fp8", [False, "expert", "row"])
+@pytest.mark.parametrize("rank", [4, 16, 40])
+def test_the_product_with_adapters_and_its_gradients_match_pytorch(is_transposed, fp8, rank):
+    from meepsquared_amd import _fp8
+
+    torch.manual_seed(0)
+    rows_per_expert = [37, 0, 200, 64, 1]
+    K, N = 96, 80
+    experts = len(rows_per_expert)
+    offsets = offsets_of(rows_per_expert)
+    x = torch.randn(sum(rows_per_expert), K, device="cuda", dtype=torch.bfloat16).requires_grad_()
+    shape = (experts, K, N) if is_transposed else (experts, N, K)
+    weight = torch.randn(shape, device="cuda", dtype=torch.bfloat16) * 0.05
+    scale = None
+    if fp8:
+        weight, scale = _fp8.quantize_stack(weight, per_row=fp8 == "row", is_transposed=is_transposed)
+    lhs, rhs = adapters(experts, K, N, rank, is_transposed)
+    bias = torch.randn(experts, N, device="cuda", dtype=torch.bfloat16)
+    got, expected = run_both(x, weight, scale, offsets, is_transposed, lhs, rhs, 2.0, bias,
+                             ref_weight=weight.float() if fp8 else None)
+    tol = Q_TOL if fp8 else BF16_TOL
+    for name, a, b in zip(("out", "grad_x", "grad_lhs", "grad_rhs"), got, expected):
+        assert a.shape == b.shape, name
+        assert rel(a, b) < tol, (name, rel(a, b))
+        # the reference's own bound (tests/test_grouped.py:141-143)
+        torch.testing.assert_close(a.float(), b.float(), atol=1e-2 * b.float().abs().max().item(), rtol=0, msg=name)
+
+
+def test_the_product_without_adapters_gives_the_base_and_its_input_gradient():
+    from meepsquared_amd import lora_linear
+
+    torch.manual_seed(0)
+    offsets = offsets_of([10, 30])
+    x = torch.randn(40, 64, device="cuda", dtype=torch.bfloat16, requires_grad=True)
+    weight = torch.randn(2, 48, 64, device="cuda", dtype=torch.bfloat16) * 0.05
+    out = lora_linear(x, weight, None, offsets, False)
+    out.sum().backward()
+    torch.testing.assert_close(out.float(), ref.reference(x.detach(), weight, offsets.cpu(), False).float(), atol=2e-2, rtol=2e-2)
+    expected = weight.sum(dim=1)[torch.repeat_interleave(torch.arange(2, device="cuda"), torch.tensor([10, 30], device="cuda"))]
+    torch.testing.assert_close(x.grad.float(), expected.float(), atol=5e-2, rtol=3e-2)
+
+
+@pytest.mark.parametrize("is_transposed", [False, True])
+def test_an_nf4_stack_computes_what_its_dequantised_twin_computes(is_transposed):
+    from meepsquared_amd import _nf4
+
+    torch.manual_seed(0)
+    rows_per_expert = [100, 0, 50, 170]
+    K, N = 128, 192
+    experts = len(rows_per_expert)
+    offsets = offsets_of(rows_per_expert)
+    x = torch.randn(sum(rows_per_expert), K, device="cuda", dtype=torch.bfloat16).requires_grad_()
+    shape = (experts, K, N) if is_transposed else (experts, N, K)
+    w = torch.randn(shape, device="cuda") * 0.02
+    stack = _nf4.quantize_stack(w)
+    twin = _nf4.dequantize_stack(stack, torch.float32)
+    lhs, rhs = adapters(experts, K, N, 16, is_transposed)
+    got, expected = run_both(x, stack, None, offsets, is_transposed, lhs, rhs, 2.0, None, ref_weight=twin)
+    for name, a, b in zip(("out", "grad_x", "grad_lhs", "grad_rhs"), got, expected):
+        assert rel(a, b) < Q_TOL, (name, rel(a, b))
+
+
+def test_the_product_is_deterministic():
+    from meepsquared_amd import lora_linear
+
+    torch.manual_seed(3)
+    offsets = offsets_of([500, 20, 700])
+    x = torch.randn(1220, 256, device="cuda", dtype=torch.bfloat16, requires_grad=True)
+    weight = torch.randn(3, 384, 256, device="cuda", dtype=torch.bfloat16) * 0.05
+    lhs, rhs = adapters(3, 256, 384, 16, False)
+    grad = torch.randn(1220, 384, device="cuda", dtype=torch.bfloat16)
+    results = []
+    for _ in range(2):
+        out = lora_linear(x, weight, None, offsets, False, lhs, rhs, 2.0)
+        out.backward(grad)
+        results.append((out.detach().clone(), x.grad.clone(), lhs.grad.clone(), rhs.grad.clone()))
+        x.grad = lhs.grad = rhs.grad = None
+    for a, b in zip(*results):
+        assert torch.equal(a, b)
+
+
+def test_qwen3_moe_sized_projection_stays_within_tolerance():
+    """Config-1 shapes (E=128, ~512 rows per expert, gate_up 2048 -> 1536, rank 16, s = 2)."""
+    from meepsquared_amd import lora_linear
+
+    torch.manual_seed(4)
+    E, K, N, r = 128, 2048, 1536, 16
+    counts = torch.multinomial(torch.ones(E), 65536, replacement=True).bincount(minlength=E)
+    offsets = torch.cumsum(counts, 0).to(torch.int32).cuda()
+    x = torch.randn(65536, K, device="cuda", dtype=torch.bfloat16, requires_grad=True)
+    weight = torch.randn(E, N, K, device="cuda", dtype=torch.bfloat16) * 0.02
+    lhs = (torch.randn(E, N, r, device="cuda") * 0.01).bfloat16().requires_grad_()
+    rhs = ((torch.rand(E, r, K, device="cuda") * 2 - 1) / K ** 0.5).bfloat16().requires_grad_()
+    got, expected = run_both(x, weight, None, offsets, False, lhs, rhs, 2.0, None)
+    for name, a, b in zip(("out", "grad_x", "grad_lhs", "grad_rhs"), got, expected):
+        assert rel(a, b) < BF16_TOL, (name, rel(a, b))

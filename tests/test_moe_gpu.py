@@ -1,0 +1,94 @@
+"""The routed MoE-LoRA layer (router -> sort -> gather -> gate_up -> SwiGLU -> down -> combine),
+forward and backward, against the oracle's composition of the reference's fp32 per-expert path."""
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import kaiming_uniform, rel
+from oracle import moe as ref_moe
+
+pytestmark = pytest.mark.gpu
+
+
+def make_layer(T, H, I, E, k, r, alpha, seed=0, is_transposed=False, sentinels=0.0):
+    """Config-0 style synthetic inputs: x, logits ~ N(0,1), W ~ N(0, 0.02), A Kaiming-uniform, B ~ N(0, 0.01)."""
+    g = torch.Generator().manual_seed(seed)
+    h = torch.randn(T, H, generator=g)
+    logits = torch.randn(T, E, generator=g)
+    gu = torch.randn(E, 2 * I, H, generator=g) * 0.02
+    dn = torch.randn(E, H, I, generator=g) * 0.02
+    f = {"gate_up_proj": (torch.randn(E, 2 * I, r, generator=g) * 0.01, kaiming_uniform((E, r, H), H, g), alpha / r),
+         "down_proj": (torch.randn(E, H, r, generator=g) * 0.01, kaiming_uniform((E, r, I), I, g), alpha / r)}
+    if is_transposed:
+        gu, dn = gu.transpose(1, 2).contiguous(), dn.transpose(1, 2).contiguous()
+        f = {n: (b.transpose(1, 2).contiguous(), a.transpose(1, 2).contiguous(), s) for n, (a, b, s) in f.items()}
+    return h, logits, gu, dn, f
+
+
+def run_layer(T, H, I, E, k, r, alpha, is_transposed=False, sentinel_frac=0.0, seed=0, fp8=None):
+    from meepsquared_amd import Experts, _fp8, routed_forward, topk_softmax
+
+    h, logits, gu, dn, f = make_layer(T, H, I, E, k, r, alpha, seed, is_transposed)
+    dev = "cuda"
+    hb = h.to(dev, torch.bfloat16).requires_grad_()
+    w, idx = topk_softmax(logits.to(dev, torch.bfloat16), k)
+    if sentinel_frac:
+        mask = torch.rand(idx.shape, generator=torch.Generator().manual_seed(9)) < sentinel_frac
+        idx = torch.where(mask.to(dev), torch.full_like(idx, E), idx)
+    w = w.detach().requires_grad_()
+    gub, dnb = gu.to(dev, torch.bfloat16), dn.to(dev, torch.bfloat16)
+    scales = {}
+    if fp8:
+        gub, s1 = _fp8.quantize_stack(gub, per_row=fp8 == "row", is_transposed=is_transposed)
+        dnb, s2 = _fp8.quantize_stack(dnb, per_row=fp8 == "row", is_transposed=is_transposed)
+        scales = {"gate_up_proj": s1, "down_proj": s2}
+    experts = Experts(gub, dnb, is_transposed, scales.get("gate_up_proj"), scales.get("down_proj"))
+    fb = {n: (a.to(dev, torch.bfloat16).requires_grad_(), b.to(dev, torch.bfloat16).requires_grad_(), s)
+          for n, (a, b, s) in f.items()}
+    out = routed_forward(experts, hb, idx, w, fb)
+    dy = torch.randn(out.shape, generator=torch.Generator().manual_seed(seed + 1)).to(dev, torch.bfloat16)
+    out.backward(dy)
+    got = {"out": out.detach(), "dh": hb.grad, "dw": w.grad}
+    for n, (a, b, _) in fb.items():
+        got[n + ".lhs"], got[n + ".rhs"] = a.grad, b.grad
+
+    # the oracle in float32 on the same (bf16-rounded) values, the fp8 stacks dequantised
+    h32 = hb.detach().float().requires_grad_()
+    w32 = w.detach().float().requires_grad_()
+    gu32, dn32 = gub.float(), dnb.float()
+    f32 = {n: (a.detach().float().requires_grad_(), b.detach().float().requires_grad_(), s) for n, (a, b, s) in fb.items()}
+    o32 = ref_moe.routed_forward(h32, idx, w32, gu32, dn32, f32, E, is_transposed, scales=scales)
+    o32.backward(dy.float())
+    want = {"out": o32.detach(), "dh": h32.grad, "dw": w32.grad}
+    for n, (a, b, _) in f32.items():
+        want[n + ".lhs"], want[n + ".rhs"] = a.grad, b.grad
+    return got, want
+
+
+@pytest.mark.parametrize("is_transposed", [False, True])
+def test_config0_layer_forward_and_backward(is_transposed):
+    # BASELINE config 0 shapes: T=512, H=256, I=512, E=8, top-2, r=8, alpha=16
+    got, want = run_layer(512, 256, 512, 8, 2, 8, 16, is_transposed)
+    for name in want:
+        assert rel(got[name], want[name]) < 1e-2, (name, rel(got[name], want[name]))
+
+
+def test_layer_with_sentinel_ids():
+    got, want = run_layer(300, 128, 64, 8, 2, 16, 32, sentinel_frac=0.1)
+    for name in want:
+        assert rel(got[name], want[name]) < 1e-2, (name, rel(got[name], want[name]))
+
+
+@pytest.mark.parametrize("fp8", ["expert", "row"])
+def test_layer_with_fp8_stacks_matches_the_dequantised_twin(fp8):
+    got, want = run_layer(512, 256, 512, 8, 2, 8, 16, fp8=fp8)
+    for name in want:
+        assert rel(got[name], want[name]) < 3e-2, (name, rel(got[name], want[name]))
+
+
+def test_qwen3_sized_layer_at_a_quarter_of_the_tokens():
+    # config 1 dims (H=2048, I=768, E=128, top-8, r=16, alpha=32) on 2048 tokens
+    got, want = run_layer(2048, 2048, 768, 128, 8, 16, 32, seed=3)
+    for name in want:
+        assert rel(got[name], want[name]) < 1e-2, (name, rel(got[name], want[name]))
