@@ -1,0 +1,227 @@
+"""MoE-LoRA layer forward + backward throughput on one MI355X: BASELINE config 1 (Qwen3-30B-A3B shaped).
+
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline]
+
+A step is one forward and backward pass of the routed MoE-LoRA layer over one batch of synthetic
+inputs already resident in HBM: router top-k softmax (from given logits), counting sort, gather,
+gate_up grouped product with its LoRA, SwiGLU, down grouped product with its LoRA, weighted
+combine; then the backward: combine, down dX with dA/dB, SwiGLU, gate_up dX with dA/dB, gather.
+Shapes: T=8192 tokens, hidden 2048, moe_intermediate 768, 128 experts, top-8 (renormalised),
+LoRA r=16, alpha=32 on gate_up and down, bf16.  Data: x, logits ~ N(0,1), W ~ N(0,0.02),
+A ~ Kaiming-uniform U(+-1/sqrt(in)), B ~ N(0,0.01), dY ~ N(0,1), seed 0.
+
+Prints one JSON line: tokens/s (whole job), ms/step, the grouped-product kernel's achieved
+TFLOP/s against the MI355X dense bf16 peak (HIP events around each of its launches inside the
+timed region, on the launch stream), and the CPU baseline: the oracle's float32 per-expert path
+(the reference's algorithm) on a bounded sample of the same workload on this host's cores.
+"""
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+T, H, I, E, K_TOP, R, ALPHA = 8192, 2048, 768, 128, 8, 16, 32
+PEAK_BF16_TFLOPS = 2500.0
+PROFILE_TRAFFIC = ROOT / "profiles" / "grouped_gemm_qwen3_traffic.txt"
+
+
+def step_flops(T, H, I, k, r):
+    """Algorithmic FLOP of one fwd+bwd: base products forward and dX (W frozen), LoRA forward, dX, dA, dB."""
+    S = T * k
+    base = 2 * S * (2 * H * 2 * I + 2 * I * H)
+    lora_fwd = 2 * S * (H * r + r * 2 * I + I * r + r * H)
+    lora_dx = 2 * S * (2 * I * r + r * H + H * r + r * I)
+    lora_da = 2 * S * (r * H + r * I)
+    lora_db = 2 * S * (2 * I * r + H * r)
+    return base + lora_fwd + lora_dx + lora_da + lora_db
+
+
+def gemm_launch_flops(info):
+    """Algorithmic FLOP of one grouped-product launch: x W plus the LoRA x A and low B."""
+    rows, K, N, r = info["rows"], info["K"], info["N"], info["rank"]
+    return 2 * rows * (K * N + K * r + r * N)
+
+
+def make_inputs(device, seed=0):
+    import torch
+
+    g = torch.Generator(device=device).manual_seed(seed)
+
+    def randn(*shape, std=1.0):
+        return torch.randn(*shape, generator=g, device=device) * std
+
+    def kaiming(*shape, fan_in):
+        return (torch.rand(*shape, generator=g, device=device) * 2 - 1) / fan_in ** 0.5
+
+    bf = torch.bfloat16
+    hidden = randn(T, H).to(bf).requires_grad_()
+    logits = randn(T, E).to(bf)
+    gate_up = randn(E, 2 * I, H, std=0.02).to(bf)
+    down = randn(E, H, I, std=0.02).to(bf)
+    s = ALPHA / R
+    factors = {"gate_up_proj": (randn(E, 2 * I, R, std=0.01).to(bf).requires_grad_(),
+                                kaiming(E, R, H, fan_in=H).to(bf).requires_grad_(), s),
+               "down_proj": (randn(E, H, R, std=0.01).to(bf).requires_grad_(),
+                             kaiming(E, R, I, fan_in=I).to(bf).requires_grad_(), s)}
+    dy = randn(T, H).to(bf)
+    return hidden, logits, gate_up, down, factors, dy
+
+
+def cpu_baseline(tokens: int):
+    """The oracle's float32 per-expert path (src/meepsquared/_grouped.py:431-444 composed as
+    src/meepsquared/_moe.py:70-126), fwd + bwd by autograd, on `tokens` tokens of the config-1
+    layer, timed on this host's cores after a small warm-up."""
+    import torch
+
+    from oracle import moe as ref_moe
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    g = torch.Generator().manual_seed(0)
+    gu = (torch.randn(E, 2 * I, H, generator=g) * 0.02).bfloat16()
+    dn = (torch.randn(E, H, I, generator=g) * 0.02).bfloat16()
+    f = {"gate_up_proj": ((torch.randn(E, 2 * I, R, generator=g) * 0.01).requires_grad_(),
+                          ((torch.rand(E, R, H, generator=g) * 2 - 1) / H ** 0.5).requires_grad_(), ALPHA / R),
+         "down_proj": ((torch.randn(E, H, R, generator=g) * 0.01).requires_grad_(),
+                       ((torch.rand(E, R, I, generator=g) * 2 - 1) / I ** 0.5).requires_grad_(), ALPHA / R)}
+
+    def run(t):
+        h = torch.randn(t, H, generator=g).bfloat16().float().requires_grad_()
+        probs = torch.softmax(torch.randn(t, E, generator=g), -1)
+        w, idx = torch.topk(probs, K_TOP)
+        w = (w / w.sum(-1, keepdim=True)).requires_grad_()
+        out = ref_moe.routed_forward(h, idx, w, gu, dn, f, E)
+        out.backward(torch.randn(t, H, generator=g))
+
+    run(64)  # warm-up: thread pool, allocator
+    t0 = time.perf_counter()
+    run(tokens)
+    dt = time.perf_counter() - t0
+    return {"value": round(tokens / dt, 2), "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": f"config-1 layer (H={H}, I={I}, E={E}, top-{K_TOP}, r={R}) fwd+bwd on {tokens} of the {T} tokens, "
+                      f"fp32 per-expert oracle, {dt:.2f} s"}
+
+
+def read_traffic():
+    """HBM bytes per launch of the grouped product from the committed rocprofv3 PMC summary, or None."""
+    if not PROFILE_TRAFFIC.exists():
+        return None
+    for line in PROFILE_TRAFFIC.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return float(line.split(":", 1)[1])
+    return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--cpu-tokens", type=int, default=T)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {a.gpus})", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from meepsquared_amd import Experts, _grouped, routed_forward, topk_softmax
+
+    torch.backends.cuda.matmul.allow_tf32 = False
+    device = "cuda:0"
+    torch.cuda.set_device(0)
+    hidden, logits, gate_up, down, factors, dy = make_inputs(device)
+    experts = Experts(gate_up, down)
+    params = [hidden] + [t for (a_, b_, _) in factors.values() for t in (a_, b_)]
+
+    def step():
+        for p in params:
+            p.grad = None
+        w, idx = topk_softmax(logits, K_TOP)
+        w.requires_grad_()
+        out = routed_forward(experts, hidden, idx, w, factors)
+        out.backward(dy)
+
+    for _ in range(a.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    launches = []  # (kind, info, start event, end event)
+
+    def observer(kind, phase, info):
+        if phase == "before":
+            ev = torch.cuda.Event(enable_timing=True)
+            ev.record()
+            launches.append([kind, dict(info), ev, None])
+        else:
+            ev = torch.cuda.Event(enable_timing=True)
+            ev.record()
+            launches[-1][3] = ev
+
+    _grouped.launch_observer = observer
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    start.record()
+    for _ in range(a.steps):
+        step()
+    end.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    _grouped.launch_observer = None
+
+    ms_per_step = start.elapsed_time(end) / a.steps
+    tokens_per_s = T * a.steps / (ms_per_step * a.steps / 1e3)
+    gemm = [(info, s.elapsed_time(e)) for kind, info, s, e in launches if kind == "grouped_gemm"]
+    red = [(info, s.elapsed_time(e)) for kind, info, s, e in launches if kind == "grouped_reduce"]
+    gemm_ms = sum(ms for _, ms in gemm)
+    gemm_flops = sum(gemm_launch_flops(info) for info, _ in gemm)
+    achieved = gemm_flops / (gemm_ms / 1e3) / 1e12
+    flops = step_flops(T, H, I, K_TOP, R)
+    per_shape = {}
+    for info, ms in gemm:
+        key = f"{info['K']}->{info['N']}"
+        per_shape.setdefault(key, []).append(ms)
+    record = {
+        "metric": "MoE-LoRA layer fwd+bwd tokens/sec; achieved TFLOP/s vs MFMA peak",
+        "value": round(tokens_per_s, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) x and logits, N(0,0.02) W, Kaiming-uniform A, N(0,0.01) B)",
+        "config": {"workload": "BASELINE config 1: Qwen3-30B-A3B-shaped MoE-LoRA layer fwd+bwd",
+                   "tokens": T, "hidden": H, "moe_intermediate": I, "experts": E, "top_k": K_TOP,
+                   "lora_rank": R, "lora_alpha": ALPHA, "parallelism": "single GPU"},
+        "step_tflops": round(flops / (ms_per_step / 1e3) / 1e12, 2),
+        "step_frac_of_bf16_peak": round(flops / (ms_per_step / 1e3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+        "roofline": {"bound": "mfma", "kernel": "grouped_gemm_kernel (4 launches per step)",
+                     "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": read_traffic()},
+        "kernel_ms_per_step": {"grouped_gemm": round(gemm_ms / a.steps, 4),
+                               "grouped_reduce": round(sum(ms for _, ms in red) / a.steps, 4),
+                               "rest": round(ms_per_step - (gemm_ms + sum(ms for _, ms in red)) / a.steps, 4)},
+        "grouped_gemm_ms_by_shape": {k_: round(sum(v) / len(v), 4) for k_, v in per_shape.items()},
+        "wall_s_timed": round(wall, 3),
+    }
+    if not a.no_cpu_baseline:
+        record["cpu_baseline"] = cpu_baseline(a.cpu_tokens)
+    else:
+        record["cpu_baseline"] = None
+    print(json.dumps(record))
+
+
+if __name__ == "__main__":
+    main()

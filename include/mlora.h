@@ -189,7 +189,8 @@ int mlora_nf4_quantize(const void* x, int x_dtype, int64_t n, const float* code,
                        uint8_t* packed, uint8_t* absmax_q, float* absmax2, float* offset,
                        void* workspace, size_t workspace_bytes, void* stream);
 
-/* y = code[nibble] · (code2[absmax_q[b]] · absmax2[b/256] + offset[0]) in y_dtype (bf16/f32). */
+/* y = code[nibble] · (code2[absmax_q[b]] · absmax2[b/256] + offset[0]) in y_dtype (bf16/f32), the absmax
+ * rounded to fp32 after the product and again after the sum (no fused multiply-add). */
 int mlora_nf4_dequantize(const uint8_t* packed, const uint8_t* absmax_q, const float* absmax2,
                          const float* offset, const float* code, const float* code2, int64_t n,
                          void* y, int y_dtype, void* stream);

@@ -26,6 +26,11 @@ from meepsquared_amd._lib import call, ptr
 BLOCK_M = 128
 RANK_MULTIPLE = 16  # the kernel's low-rank MFMAs take the rank in blocks of 16
 
+# For measurement only: when set, called as launch_observer(kernel, phase, info) with phase
+# "before"/"after" around each product or reduction launch, on the launching thread (the launch
+# goes to torch's current stream); info holds the launch's sizes.  None in normal use.
+launch_observer = None
+
 
 def max_tiles(rows: int, experts: int, block_m: int = BLOCK_M) -> int:
     """An upper bound on the tiles: every expert's last tile may be partial (_grouped.py:83-85)."""
@@ -169,6 +174,9 @@ def _launch(x, weight, scale, offsets, is_transposed, adapters, scaling, bias, s
     at = bt = None
     if adapters is not None:
         at, bt = adapters.at, adapters.bt
+    info = {"rows": rows, "K": K, "N": N, "rank": adapters.rank if adapters is not None else 0}
+    if launch_observer is not None:
+        launch_observer("grouped_gemm", "before", info)
     call("mlora_grouped_gemm",
          ptr(x), x.stride(0), rows, K, N,
          w_ptr, w_dtype, w_se, w_sk, w_sn,
@@ -180,6 +188,8 @@ def _launch(x, weight, scale, offsets, is_transposed, adapters, scaling, bias, s
          ptr(bias), bias.stride(0) if bias is not None else 0,
          ptr(out), out.stride(0), ptr(low), low.stride(0) if low is not None else 0,
          ptr(offsets), offsets.numel(), _lib.stream(x.device))
+    if launch_observer is not None:
+        launch_observer("grouped_gemm", "after", info)
     return out, low
 
 
@@ -210,8 +220,13 @@ def _reduce(g: torch.Tensor, low: torch.Tensor, offsets: torch.Tensor, scaling: 
     if g.stride(1) != 1 or g.stride(0) % 8 or g.data_ptr() % 16:
         g = g.contiguous()
     out = torch.empty((experts, N, R), device=g.device, dtype=torch.bfloat16)
+    info = {"rows": rows, "N": N, "R": R}
+    if launch_observer is not None:
+        launch_observer("grouped_reduce", "before", info)
     call("mlora_grouped_reduce", ptr(g), g.stride(0), ptr(low), low.stride(0), rows, N, R, float(scaling),
          ptr(offsets), experts, ptr(out), out.stride(0), out.stride(1), out.stride(2), _lib.stream(g.device))
+    if launch_observer is not None:
+        launch_observer("grouped_reduce", "after", info)
     return out
 
 

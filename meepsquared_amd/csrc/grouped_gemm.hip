@@ -122,7 +122,9 @@ __device__ __forceinline__ u32x4 nf4x8_to_bf16(uint32_t v, float absmax, const f
   }
   return r;
 }
+// a block's absmax: code2[q] * absmax2 + offset, rounded after the product and after the sum (no fma)
 __device__ __forceinline__ float nf4_block_absmax(const GemmArgs& p, int64_t block) {
+#pragma clang fp contract(off)
   return p.nf4_code2[p.nf4_q[block]] * p.nf4_absmax2[block >> 8] + p.nf4_offset[0];
 }
 

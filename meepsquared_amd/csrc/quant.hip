@@ -12,6 +12,9 @@
 
 #include "common.hpp"
 
+// Bit-exact definitions: no multiply-add contraction anywhere in this file.
+#pragma clang fp contract(off)
+
 namespace mlora {
 
 // fp32 -> OCP e4m3fn with round-to-nearest-even.  Magnitudes from 464 up (and NaN) give NaN
@@ -191,7 +194,7 @@ __global__ __launch_bounds__(256) void nf4_dequant_kernel(const uint8_t* __restr
                                                           T* __restrict__ y) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
     const int64_t b = i >> 6;
-    const float a = code2[absmax_q[b]] * absmax2[b >> 8] + offset[0];
+    const float a = code2[absmax_q[b]] * absmax2[b >> 8] + offset[0];  // two roundings (contraction is off)
     const uint32_t byte = packed[i >> 1];
     const uint32_t nib = (i & 1) ? (byte & 0xFu) : (byte >> 4);
     stf(y, i, code[nib] * a);
