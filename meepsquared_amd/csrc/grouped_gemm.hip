@@ -30,66 +30,34 @@
 #include <mutex>
 #include <unordered_map>
 
-#include "common.hpp"
+#include "gemm_common.hpp"
 
 namespace mlora {
 
-constexpr int BM = 128, BN = 128, BK = 64;
-constexpr int BKP = BK + 8;  // LDS row pitch in bf16: rows 144 bytes apart keep ds_read_b128 free of conflicts
-constexpr int kThreads = 256;
-constexpr int WAVES_N = 2;
-constexpr int WTM = 64, WTN = 64;   // each wave's corner
-constexpr int FM = WTM / 32, FN = WTN / 32;
-constexpr int kMaxRank = 64;
-constexpr int kXcds = 8;
-constexpr uint32_t kOob = 0x80000000u;  // an offset past every resource's end: the load returns zero
-
-enum { W_BF16 = 0, W_FP8 = 1, W_NF4 = 2 };
-
-struct GemmArgs {
-  const bf16* x;
-  int64_t ldx;
-  const uint8_t* w;      // bytes
-  int64_t w_se, w_sk, w_sn;  // elements
-  const float* scale;
-  int64_t scale_se;
-  int scale_kind;
-  const uint8_t* nf4_q;
-  const float* nf4_absmax2;
-  const float* nf4_code2;
-  const float* nf4_offset;
-  const float* nf4_code;
-  const bf16* at;        // A_e^T: [e][r][k], k contiguous
-  int64_t at_se, at_sr;
-  const bf16* bt;        // B_e^T: [e][n][r], r contiguous
-  int64_t bt_se, bt_sn;
-  int rank;              // a multiple of 16
-  float scaling;
-  const bf16* bias;
-  int64_t bias_se;
-  bf16* out;
-  int64_t ldo;
-  bf16* low;
-  int64_t ldl;
-  const int32_t* offsets;
-  int64_t rows;
-  int E, K, N;
-};
-
-typedef __amdgpu_buffer_rsrc_t rsrc_t;
-
-__device__ __forceinline__ rsrc_t make_rsrc(const void* base, int64_t bytes) {
-  const int64_t cap = 0x7FFFFFF0;
-  return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, (int)(bytes < cap ? bytes : cap), 0x00020000);
-}
-__device__ __forceinline__ u32x4 ld128(rsrc_t r, uint32_t off) {
-  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
-}
-__device__ __forceinline__ u32x2 ld64(rsrc_t r, uint32_t off) {
-  return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
-}
-__device__ __forceinline__ uint32_t ld32(rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0); }
-
+// Tile shape: a workgroup computes BM x BN of the output with WAVES_M x WAVES_N waves; OCC is the
+// number of waves per SIMD the register budget is sized for.  (Compile-time; the defaults are the
+// shape measured fastest on the config-1 products.)
+#ifndef MLORA_BM
+#define MLORA_BM 256
+#endif
+#ifndef MLORA_BN
+#define MLORA_BN 256
+#endif
+#ifndef MLORA_WAVES_M
+#define MLORA_WAVES_M 2
+#endif
+#ifndef MLORA_WAVES_N
+#define MLORA_WAVES_N 2
+#endif
+#ifndef MLORA_OCC
+#define MLORA_OCC 1
+#endif
+constexpr int BM = MLORA_BM, BN = MLORA_BN, BK = 64;
+constexpr int WAVES_M = MLORA_WAVES_M, WAVES_N = MLORA_WAVES_N;
+constexpr int kThreads = 64 * WAVES_M * WAVES_N;
+constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;  // each wave's share of the tile
+constexpr int FM = WTM / 32, FN = WTN / 32;            // its 32 x 32 MFMA blocks
+static_assert(FM >= 1 && FN >= 1 && (2 * FM) % WAVES_N == 0, "tile shape");
 __device__ __forceinline__ uint32_t lo_pair(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x05040100u); }
 __device__ __forceinline__ uint32_t hi_pair(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x07060302u); }
 
@@ -136,33 +104,44 @@ __device__ __forceinline__ uint32_t w_bytes(int64_t el) {
   else return (uint32_t)(el >> 1);
 }
 
+// LDS tiles are [row][k] with rows of BK = 64 bf16 (128 bytes) and no padding; the 16-byte chunk c of
+// row r sits in slot c ^ ((r >> 1) & 7).  An MFMA operand read serves 16 lanes on 16 consecutive rows
+// at one chunk per cycle: two rows share each 256-byte bank line, and the XOR gives the 16 reads 16
+// distinct 16-byte bank groups; the stage writes (8 lanes per row) stay conflict-free as well.
+__device__ __forceinline__ int swz(int row, int chunk) { return row * BK + ((chunk ^ ((row >> 1) & 7)) << 3); }
+
 // One BK-deep stage: the global loads land in registers (issued a stage ahead) and are decoded
 // into LDS after the current stage's MFMAs.
 template <int WDT, bool BKC, bool SCALE_K, int NRB>
 struct Stage {
-  static constexpr int kAChunks = NRB * 16 * BK / 8;  // 16-byte chunks of A^T per stage
+  static constexpr int kXChunks = BM * BK / 8;                                // 16-byte chunks of x per stage
+  static constexpr int kXPer = (kXChunks + kThreads - 1) / kThreads;
+  static constexpr int kWUnits = BKC ? BN * BK / 8 : (BK / 4) * (BN / 8);       // W chunks, or 4(k) x 8(n) blocks
+  static constexpr int kWPer = (kWUnits + kThreads - 1) / kThreads;
+  static constexpr int kWVec = BKC ? kWPer : kWPer * 4;                         // W vectors per thread
+  static constexpr int kAChunks = NRB * 16 * BK / 8;                                      // A^T chunks per stage
   static constexpr int kAPer = (kAChunks + kThreads - 1) / kThreads;
-  u32x4 x[4];
-  u32x4 w16[4];
-  u32x2 w8[4];
-  uint32_t w4[4];
-  float ws[BKC && SCALE_K ? 32 : 4];
+  u32x4 x[kXPer];
+  u32x4 w16[kWVec];
+  u32x2 w8[kWVec];
+  uint32_t w4[kWVec];
+  float ws[BKC && SCALE_K ? kWVec * 8 : kWVec];
   u32x4 a[kAPer > 0 ? kAPer : 1];
 
   __device__ __forceinline__ void load(const GemmArgs& p, rsrc_t rx, rsrc_t rw, rsrc_t ra, int e, int n0, int k0,
                                        int tid) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < kXPer; ++i) {
       const int c = tid + i * kThreads;
       const int rr = c >> 3, k = k0 + (c & 7) * 8;
-      x[i] = ld128(rx, k < p.K ? (uint32_t)((rr * p.ldx + k) * 2) : kOob);
+      if (c < kXChunks) x[i] = ld128(rx, k < p.K ? (uint32_t)((rr * p.ldx + k) * 2) : kOob);
     }
     if constexpr (BKC) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < kWPer; ++i) {
         const int c = tid + i * kThreads;
         const int n = n0 + (c >> 3), k = k0 + (c & 7) * 8;
-        const bool ok = n < p.N && k < p.K;
+        const bool ok = c < kWUnits && n < p.N && k < p.K;
         const int64_t el = (int64_t)n * p.w_sn + k;
         const uint32_t off = ok ? w_bytes<WDT>(el) : kOob;
         if constexpr (WDT == W_BF16) {
@@ -179,21 +158,26 @@ struct Stage {
         }
       }
     } else {
-      const int kb = tid & 15, n = n0 + (tid >> 4) * 8;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int k = k0 + kb * 4 + q;
-        const bool ok = n < p.N && k < p.K;
-        const int64_t el = (int64_t)k * p.w_sk + n;
-        const uint32_t off = ok ? w_bytes<WDT>(el) : kOob;
-        if constexpr (WDT == W_BF16) {
-          w16[q] = ld128(rw, off);
-        } else if constexpr (WDT == W_FP8) {
-          w8[q] = ld64(rw, off);
-          if constexpr (SCALE_K) ws[q] = ok ? p.scale[(int64_t)e * p.scale_se + k] : 0.f;
-        } else {
-          w4[q] = ld32(rw, off);
-          ws[q] = ok ? nf4_block_absmax(p, ((int64_t)e * p.w_se + el) >> 6) : 0.f;
+      for (int b = 0; b < kWPer; ++b) {
+        const int blk = tid + b * kThreads;
+        const int kb = blk & 15, n = n0 + (blk >> 4) * 8;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int k = k0 + kb * 4 + q;
+          const bool ok = blk < kWUnits && n < p.N && k < p.K;
+          const int64_t el = (int64_t)k * p.w_sk + n;
+          const uint32_t off = ok ? w_bytes<WDT>(el) : kOob;
+          const int v = b * 4 + q;
+          if constexpr (WDT == W_BF16) {
+            w16[v] = ld128(rw, off);
+          } else if constexpr (WDT == W_FP8) {
+            w8[v] = ld64(rw, off);
+            if constexpr (SCALE_K) ws[v] = ok ? p.scale[(int64_t)e * p.scale_se + k] : 0.f;
+          } else {
+            w4[v] = ld32(rw, off);
+            ws[v] = ok ? nf4_block_absmax(p, ((int64_t)e * p.w_se + el) >> 6) : 0.f;
+          }
         }
       }
     }
@@ -209,69 +193,138 @@ struct Stage {
 
   __device__ __forceinline__ void store(bf16* As, bf16* Bs, bf16* Aa, const float* code, int tid) const {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < kXPer; ++i) {
       const int c = tid + i * kThreads;
-      *(u32x4*)(As + (c >> 3) * BKP + (c & 7) * 8) = x[i];
+      if (c < kXChunks) *(u32x4*)(As + swz(c >> 3, c & 7)) = x[i];
     }
     if constexpr (BKC) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < kWPer; ++i) {
         const int c = tid + i * kThreads;
+        if (c >= kWUnits) continue;
         u32x4 v;
         if constexpr (WDT == W_BF16) v = w16[i];
         else if constexpr (WDT == W_FP8) v = SCALE_K ? fp8x8_to_bf16_scaled(w8[i], ws + i * 8) : fp8x8_to_bf16(w8[i], 1.0f);
         else v = nf4x8_to_bf16(w4[i], ws[i], code);
-        *(u32x4*)(Bs + (c >> 3) * BKP + (c & 7) * 8) = v;
+        *(u32x4*)(Bs + swz(c >> 3, c & 7)) = v;
       }
     } else {
-      const int kb = tid & 15, nb8 = tid >> 4;
-      u32x4 row[4];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        if constexpr (WDT == W_BF16) row[q] = w16[q];
-        else if constexpr (WDT == W_FP8) row[q] = fp8x8_to_bf16(w8[q], SCALE_K ? ws[q] : 1.0f);
-        else row[q] = nf4x8_to_bf16(w4[q], ws[q], code);
-      }
-      // transpose 4 (k) x 8 (n) into 8 rows (n) of 4 k
+      for (int b = 0; b < kWPer; ++b) {
+        const int blk = tid + b * kThreads;
+        if (blk >= kWUnits) continue;
+        const int kb = blk & 15, nb8 = blk >> 4;
+        u32x4 row[4];
 #pragma unroll
-      for (int m = 0; m < 4; ++m) {
-        u32x2 ev, od;
-        ev[0] = lo_pair(row[0][m], row[1][m]);
-        ev[1] = lo_pair(row[2][m], row[3][m]);
-        od[0] = hi_pair(row[0][m], row[1][m]);
-        od[1] = hi_pair(row[2][m], row[3][m]);
-        *(u32x2*)(Bs + (nb8 * 8 + 2 * m) * BKP + kb * 4) = ev;
-        *(u32x2*)(Bs + (nb8 * 8 + 2 * m + 1) * BKP + kb * 4) = od;
+        for (int q = 0; q < 4; ++q) {
+          const int v = b * 4 + q;
+          if constexpr (WDT == W_BF16) row[q] = w16[v];
+          else if constexpr (WDT == W_FP8) row[q] = fp8x8_to_bf16(w8[v], SCALE_K ? ws[v] : 1.0f);
+          else row[q] = nf4x8_to_bf16(w4[v], ws[v], code);
+        }
+        // transpose 4 (k) x 8 (n) into 8 rows (n) of 4 k: 8 bytes at k = kb*4, in chunk kb/2
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          u32x2 ev, od;
+          ev[0] = lo_pair(row[0][m], row[1][m]);
+          ev[1] = lo_pair(row[2][m], row[3][m]);
+          od[0] = hi_pair(row[0][m], row[1][m]);
+          od[1] = hi_pair(row[2][m], row[3][m]);
+          const int n_ev = nb8 * 8 + 2 * m, n_od = n_ev + 1;
+          *(u32x2*)(Bs + swz(n_ev, kb >> 1) + (kb & 1) * 4) = ev;
+          *(u32x2*)(Bs + swz(n_od, kb >> 1) + (kb & 1) * 4) = od;
+        }
       }
     }
     if constexpr (NRB > 0) {
 #pragma unroll
       for (int i = 0; i < kAPer; ++i) {
         const int c = tid + i * kThreads;
-        if (c < kAChunks) *(u32x4*)(Aa + (c >> 3) * BKP + (c & 7) * 8) = a[i];
+        if (c < kAChunks) *(u32x4*)(Aa + swz(c >> 3, c & 7)) = a[i];
       }
     }
   }
 };
 
-// NRB = rank / 16 (0: no adapters).
+constexpr int kLS = 2 * FM / WAVES_N;  // 16-row halves of x·A_e per wave
+
+// The K loop of one work item for a wave with AM live row blocks (of FM): every MFMA of the loop
+// is unconditional, so the compiler can interleave operand reads, MFMAs and the next stage's loads.
+template <int AM, int WDT, bool BKC, bool SCALE_K, int NRB>
+__device__ __forceinline__ void kloop(const GemmArgs& p, Stage<WDT, BKC, SCALE_K, NRB>& st, rsrc_t rx, rsrc_t rw,
+                                      rsrc_t ra, int e, int n0, int nk, bf16* As, bf16* Bs, bf16* Aa,
+                                      const float* code, int tid, int lane, int wm, int wn, f32x16 (&acc)[FM][FN],
+                                      f32x4 (&lacc)[kLS][NRB > 0 ? NRB : 1]) {
+  constexpr int RP = NRB * 16;
+  for (int kt = 0; kt < nk; ++kt) {
+    const int buf = kt & 1;
+    if (kt + 1 < nk) st.load(p, rx, rw, ra, e, n0, (kt + 1) * BK, tid);
+    const bf16* as = As + buf * BM * BK;
+    const bf16* bs = Bs + buf * BN * BK;
+    if constexpr (AM > 0) {
+#pragma unroll
+      for (int kk = 0; kk < BK / 16; ++kk) {
+        bf16x8 af[AM], bfr[FN];
+        const int ch = kk * 2 + (lane >> 5);
+#pragma unroll
+        for (int i = 0; i < AM; ++i) af[i] = *(const bf16x8*)(as + swz((i * WAVES_M + wm) * 32 + (lane & 31), ch));
+#pragma unroll
+        for (int j = 0; j < FN; ++j) bfr[j] = *(const bf16x8*)(bs + swz((j * WAVES_N + wn) * 32 + (lane & 31), ch));
+#pragma unroll
+        for (int i = 0; i < AM; ++i)
+#pragma unroll
+          for (int j = 0; j < FN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[j], af[i], acc[i][j], 0, 0, 0);
+      }
+      if constexpr (NRB > 0) {
+        const bf16* aa = Aa + buf * RP * BK;
+#pragma unroll
+        for (int kk = 0; kk < BK / 32; ++kk) {
+          const int ch = kk * 4 + (lane >> 4);
+          bf16x8 af[NRB];
+#pragma unroll
+          for (int rb = 0; rb < NRB; ++rb) af[rb] = *(const bf16x8*)(aa + swz(rb * 16 + (lane & 15), ch));
+#pragma unroll
+          for (int q = 0; q < kLS; ++q) {
+            const int sh = wn + WAVES_N * q;  // this wave's 16-row half: block sh / 2, half sh % 2
+            if ((sh >> 1) < AM) {  // wn is wave-uniform: a scalar branch around whole MFMA groups
+              const int rbase = ((sh >> 1) * WAVES_M + wm) * 32 + (sh & 1) * 16;
+              const bf16x8 xf = *(const bf16x8*)(as + swz(rbase + (lane & 15), ch));
+#pragma unroll
+              for (int rb = 0; rb < NRB; ++rb)
+                lacc[q][rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf, af[rb], lacc[q][rb], 0, 0, 0);
+            }
+          }
+        }
+      }
+    }
+    if (kt + 1 < nk) st.store(As + (buf ^ 1) * BM * BK, Bs + (buf ^ 1) * BN * BK, Aa + (buf ^ 1) * RP * BK, code, tid);
+    __syncthreads();
+  }
+}
+
+// NRB = rank / 16 (0: no adapters).  Wave (wm, wn) owns the 32-row blocks i*WAVES_M + wm and the
+// 32-column blocks j*WAVES_N + wn of the tile (interleaved, so a tile cut short by the end of an
+// expert's rows still spreads its rows over every wave); blocks past the expert's last row or
+// past N are skipped, MFMAs included.
 template <int WDT, bool BKC, bool SCALE_K, int NRB>
-__global__ __launch_bounds__(kThreads, 2) void grouped_gemm_kernel(GemmArgs p) {
+__global__ __launch_bounds__(kThreads, MLORA_OCC) void grouped_gemm_kernel(GemmArgs p) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
   constexpr int RP = NRB * 16;
   constexpr int LP = RP + 8;  // pitch of the epilogue's low and B^T tiles
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: branches on it stay scalar
   const int wm = wave / WAVES_N, wn = wave % WAVES_N;
   const int E = p.E;
 
-  bf16* As = (bf16*)smem;                    // [2][BM][BKP]
-  bf16* Bs = As + 2 * BM * BKP;              // [2][BN][BKP]
-  bf16* Aa = Bs + 2 * BN * BKP;              // [2][RP][BKP]
-  int* starts = (int*)(Aa + 2 * RP * BKP);   // E + 1
+  bf16* As = (bf16*)smem;                    // [2][BM][BK] swizzled
+  bf16* Bs = As + 2 * BM * BK;               // [2][BN][BK] swizzled
+  bf16* Aa = Bs + 2 * BN * BK;               // [2][RP][BK] swizzled
+  int* starts = (int*)(Aa + 2 * RP * BK);    // E + 1
   int* tstart = starts + (E + 1);            // E + 1
   float* code = (float*)(tstart + (E + 1));  // 16 (NF4 code book)
   bf16* Ls = As;                             // epilogue: [BM][LP], aliasing the x stages
-  bf16* Lb = As + BM * LP;                   // epilogue: [BN][LP]
+  bf16* Lb = Bs;                             // epilogue: [BN][LP], aliasing the W stages
 
   // ---- the tile map, from offsets ----
   // row starts clamped into [0, rows]: offsets past the end of x (a caller's mistake) cannot send a
@@ -284,7 +337,10 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_kernel(GemmArgs p) {
     if (tid < 16) code[tid] = p.nf4_code[tid];
   }
   __syncthreads();
-  for (int e = tid; e < E; e += kThreads) tstart[e] = max(starts[e + 1] - starts[e], 0) / BM + ((max(starts[e + 1] - starts[e], 0) % BM) != 0);
+  for (int e = tid; e < E; e += kThreads) {
+    const int c = max(starts[e + 1] - starts[e], 0);
+    tstart[e] = (c + BM - 1) / BM;
+  }
   __syncthreads();
   if (wave == 0) {  // exclusive scan of tstart[0..E), 64 at a time
     int run = 0;
@@ -304,7 +360,7 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_kernel(GemmArgs p) {
   }
   __syncthreads();
   const int nb = (p.N + BN - 1) / BN;
-  const int64_t total = (int64_t)tstart[E] * nb;
+  const int64_t total = (int64_t)__builtin_amdgcn_readfirstlane(tstart[E]) * nb;
   const int xcd = blockIdx.x % kXcds, slot = blockIdx.x / kXcds, per_xcd = gridDim.x / kXcds;
   const int64_t chunk = (total + kXcds - 1) / kXcds;
   const int64_t beg = xcd * chunk, end = min(beg + chunk, total);
@@ -317,14 +373,22 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_kernel(GemmArgs p) {
       const int mid = (lo + hi + 1) >> 1;
       if (tstart[mid] <= t) lo = mid; else hi = mid - 1;
     }
-    const int e = lo;
-    const int64_t row0 = (int64_t)starts[e] + (int64_t)(t - tstart[e]) * BM;
-    const int mrows = (int)min((int64_t)BM, (int64_t)starts[e + 1] - row0);
+    // values read from LDS are per-lane to the compiler: make the tile's scalars wave-uniform (SGPRs)
+    const int e = __builtin_amdgcn_readfirstlane(lo);
+    const int e_start = __builtin_amdgcn_readfirstlane(starts[e]);
+    const int e_end = __builtin_amdgcn_readfirstlane(starts[e + 1]);
+    const int e_t0 = __builtin_amdgcn_readfirstlane(tstart[e]);
+    const int64_t row0 = (int64_t)e_start + (int64_t)(t - e_t0) * BM;
+    const int mrows = (int)min((int64_t)BM, (int64_t)e_end - row0);
     const int n0 = nblk * BN;
+    const int ncols = min(BN, p.N - n0);
+    // this wave's live blocks: a prefix of its interleaved row and column blocks
+    const int mb = (mrows + 31) >> 5, nbk = (ncols + 31) >> 5;
+    const int am = min(FM, max(0, (mb - wm + WAVES_M - 1) / WAVES_M));
+    const int an = min(FN, max(0, (nbk - wn + WAVES_N - 1) / WAVES_N));
 
-    // resources: x from this tile's first row to at most BM rows on; W and A^T of expert e
-    const int64_t xrows = min((int64_t)BM, p.rows - row0);
-    const rsrc_t rx = make_rsrc(p.x + row0 * p.ldx, xrows * p.ldx * 2);
+    // resources: the tile's own rows of x (rows past the expert read as zero); W, A^T of expert e
+    const rsrc_t rx = make_rsrc(p.x + row0 * p.ldx, (int64_t)mrows * p.ldx * 2);
     const int64_t we = (int64_t)e * p.w_se;
     const rsrc_t rw = WDT == W_BF16 ? make_rsrc(p.w + we * 2, p.w_se * 2)
                     : WDT == W_FP8  ? make_rsrc(p.w + we, p.w_se)
@@ -337,11 +401,13 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_kernel(GemmArgs p) {
     for (int i = 0; i < FM; ++i)
 #pragma unroll
       for (int j = 0; j < FN; ++j) acc[i][j] = f32x16{};
-    f32x4 lacc[2][NRB > 0 ? NRB : 1];
+    // x·A_e: the 16-row halves s = 0 .. 2*FM-1 of this wave-row's blocks (block s/2, half s%2) are
+    // shared among its WAVES_N waves: this wave takes s = wn + WAVES_N*q
+    f32x4 lacc[kLS][NRB > 0 ? NRB : 1];
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
+    for (int q = 0; q < kLS; ++q)
 #pragma unroll
-      for (int j = 0; j < (NRB > 0 ? NRB : 1); ++j) lacc[h][j] = f32x4{};
+      for (int j = 0; j < (NRB > 0 ? NRB : 1); ++j) lacc[q][j] = f32x4{};
 
     Stage<WDT, BKC, SCALE_K, NRB> st;
     __syncthreads();  // the previous item's epilogue is done with the LDS
@@ -349,70 +415,50 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_kernel(GemmArgs p) {
     st.store(As, Bs, Aa, code, tid);
     __syncthreads();
 
-    for (int kt = 0; kt < nk; ++kt) {
-      const int buf = kt & 1;
-      if (kt + 1 < nk) st.load(p, rx, rw, ra, e, n0, (kt + 1) * BK, tid);
-      const bf16* as = As + buf * BM * BKP;
-      const bf16* bs = Bs + buf * BN * BKP;
-#pragma unroll
-      for (int kk = 0; kk < BK / 16; ++kk) {
-        bf16x8 af[FM], bfr[FN];
-#pragma unroll
-        for (int i = 0; i < FM; ++i)
-          af[i] = *(const bf16x8*)(as + (wm * WTM + i * 32 + (lane & 31)) * BKP + kk * 16 + (lane >> 5) * 8);
-#pragma unroll
-        for (int j = 0; j < FN; ++j)
-          bfr[j] = *(const bf16x8*)(bs + (wn * WTN + j * 32 + (lane & 31)) * BKP + kk * 16 + (lane >> 5) * 8);
-#pragma unroll
-        for (int i = 0; i < FM; ++i)
-#pragma unroll
-          for (int j = 0; j < FN; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
-      }
-      if constexpr (NRB > 0) {
-        const bf16* aa = Aa + buf * RP * BKP;
-        const int lr0 = wm * WTM + wn * 32;  // this wave's 32 rows of x·A_e
-#pragma unroll
-        for (int kk = 0; kk < BK / 32; ++kk) {
-          bf16x8 xf[2];
-#pragma unroll
-          for (int h = 0; h < 2; ++h)
-            xf[h] = *(const bf16x8*)(as + (lr0 + h * 16 + (lane & 15)) * BKP + kk * 32 + (lane >> 4) * 8);
-#pragma unroll
-          for (int rb = 0; rb < NRB; ++rb) {
-            const bf16x8 af = *(const bf16x8*)(aa + (rb * 16 + (lane & 15)) * BKP + kk * 32 + (lane >> 4) * 8);
-#pragma unroll
-            for (int h = 0; h < 2; ++h)
-              lacc[h][rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf[h], af, lacc[h][rb], 0, 0, 0);
-          }
-        }
-      }
-      if (kt + 1 < nk)
-        st.store(As + (buf ^ 1) * BM * BKP, Bs + (buf ^ 1) * BN * BKP, Aa + (buf ^ 1) * RP * BKP, code, tid);
-      __syncthreads();
+    switch (am) {  // the K loop, specialised on this wave's live row blocks: no branches inside
+      case FM: kloop<FM, WDT, BKC, SCALE_K, NRB>(p, st, rx, rw, ra, e, n0, nk, As, Bs, Aa, code, tid, lane, wm, wn, acc, lacc); break;
+#if MLORA_BM / MLORA_WAVES_M / 32 >= 4
+      case 3: kloop<3, WDT, BKC, SCALE_K, NRB>(p, st, rx, rw, ra, e, n0, nk, As, Bs, Aa, code, tid, lane, wm, wn, acc, lacc); break;
+#endif
+#if MLORA_BM / MLORA_WAVES_M / 32 >= 3
+      case 2: kloop<2, WDT, BKC, SCALE_K, NRB>(p, st, rx, rw, ra, e, n0, nk, As, Bs, Aa, code, tid, lane, wm, wn, acc, lacc); break;
+#endif
+#if MLORA_BM / MLORA_WAVES_M / 32 >= 2
+      case 1: kloop<1, WDT, BKC, SCALE_K, NRB>(p, st, rx, rw, ra, e, n0, nk, As, Bs, Aa, code, tid, lane, wm, wn, acc, lacc); break;
+#endif
+      default: kloop<0, WDT, BKC, SCALE_K, NRB>(p, st, rx, rw, ra, e, n0, nk, As, Bs, Aa, code, tid, lane, wm, wn, acc, lacc); break;
     }
 
     // ---- epilogue ----
-    float cscale[FN];
+    // acc[i][j] holds out^T of the 32 x 32 block (i, j): lane l has the tile row (i*WAVES_M + wm)*32 + l%32
+    // and, for value v, the column (j*WAVES_N + wn)*32 + 8*(v/4) + 4*(l/32) + v%4: four runs of four.
+    const int col_l = 4 * (lane >> 5);
+    f32x4 cs[FN][4];  // the base product's scale per column
 #pragma unroll
-    for (int j = 0; j < FN; ++j) {
-      float c = 1.0f;
-      if (p.scale_kind == MLORA_SCALE_EXPERT) c = p.scale[e];
-      else if (p.scale_kind == MLORA_SCALE_ROW && !SCALE_K) {
-        const int n = n0 + wn * WTN + j * 32 + (lane & 31);
-        c = n < p.N ? p.scale[(int64_t)e * p.scale_se + n] : 0.f;
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        if (p.scale_kind == MLORA_SCALE_EXPERT) {
+          const float c = p.scale[e];
+          cs[j][g] = f32x4{c, c, c, c};
+        } else if (p.scale_kind == MLORA_SCALE_ROW && !SCALE_K) {
+          const int n = n0 + (j * WAVES_N + wn) * 32 + 8 * g + col_l;
+          cs[j][g] = n < p.N ? *(const f32x4*)(p.scale + (int64_t)e * p.scale_se + n) : f32x4{};
+        } else {
+          cs[j][g] = f32x4{1.f, 1.f, 1.f, 1.f};
+        }
       }
-      cscale[j] = c;
-    }
     if constexpr (NRB > 0) {
-      const int lr0 = wm * WTM + wn * 32;
 #pragma unroll
-      for (int h = 0; h < 2; ++h)
+      for (int q = 0; q < kLS; ++q) {
+        const int sh = wn + WAVES_N * q;
+        const int rbase = ((sh >> 1) * WAVES_M + wm) * 32 + (sh & 1) * 16;
 #pragma unroll
         for (int rb = 0; rb < NRB; ++rb)
 #pragma unroll
           for (int v = 0; v < 4; ++v)
-            Ls[(lr0 + h * 16 + 4 * (lane >> 4) + v) * LP + rb * 16 + (lane & 15)] = (bf16)lacc[h][rb][v];
+            Ls[(rbase + 4 * (lane >> 4) + v) * LP + rb * 16 + (lane & 15)] = (bf16)lacc[q][rb][v];
+      }
       // B_e^T rows n0 .. n0+BN: Lb[n][r]
       const rsrc_t rbt = make_rsrc(p.bt + (int64_t)e * p.bt_se, (int64_t)p.N * p.bt_sn * 2);
       for (int c = tid; c < BN * RP / 8; c += kThreads) {
@@ -427,54 +473,58 @@ __global__ __launch_bounds__(kThreads, 2) void grouped_gemm_kernel(GemmArgs p) {
           if (m < mrows) *(u32x4*)(p.low + (row0 + m) * p.ldl + rc) = *(const u32x4*)(Ls + m * LP + rc);
         }
       }
-      if (p.scaling != 0.f) {
-        // out = s · (c/s · x W + low B): the low-rank product joins the accumulator through one MFMA
-        const float inv_s = 1.0f / p.scaling;
-#pragma unroll
-        for (int i = 0; i < FM; ++i)
-#pragma unroll
-          for (int j = 0; j < FN; ++j) acc[i][j] *= cscale[j] * inv_s;
-#pragma unroll
-        for (int rk = 0; rk < NRB; ++rk) {
-          bf16x8 lf[FM], bfr[FN];
-#pragma unroll
-          for (int i = 0; i < FM; ++i)
-            lf[i] = *(const bf16x8*)(Ls + (wm * WTM + i * 32 + (lane & 31)) * LP + rk * 16 + (lane >> 5) * 8);
-#pragma unroll
-          for (int j = 0; j < FN; ++j)
-            bfr[j] = *(const bf16x8*)(Lb + (wn * WTN + j * 32 + (lane & 31)) * LP + rk * 16 + (lane >> 5) * 8);
-#pragma unroll
-          for (int i = 0; i < FM; ++i)
-#pragma unroll
-            for (int j = 0; j < FN; ++j)
-              acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(lf[i], bfr[j], acc[i][j], 0, 0, 0);
-        }
-#pragma unroll
-        for (int j = 0; j < FN; ++j) cscale[j] = p.scaling;
-      }
     }
+    // Block by block: out = c · acc + s · bf16(x·A_e)·B_e (one MFMA chain of depth R into a
+    // temporary) + bias, stored 8 bytes (four consecutive columns of one row) per lane and group.
+    const bool lora_on = NRB > 0 && p.scaling != 0.f;
 #pragma unroll
-    for (int j = 0; j < FN; ++j) {
-      const int n = n0 + wn * WTN + j * 32 + (lane & 31);
-      if (n >= p.N) continue;
-      const float bias = p.bias != nullptr ? (float)p.bias[(int64_t)e * p.bias_se + n] : 0.f;
-      bf16* o = p.out + row0 * p.ldo + n;
+    for (int i = 0; i < FM; ++i) {
+      const int row = (i * WAVES_M + wm) * 32 + (lane & 31);
+      if (i >= am) continue;
+      bf16* orow = p.out + (row0 + row) * p.ldo;
 #pragma unroll
-      for (int i = 0; i < FM; ++i)
+      for (int j = 0; j < FN; ++j) {
+        if (j >= an) continue;
+        f32x16 t = f32x16{};
+        if constexpr (NRB > 0) {
+          if (lora_on) {
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int row = wm * WTM + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-          if (row < mrows) o[row * p.ldo] = (bf16)(acc[i][j][v] * cscale[j] + bias);
+            for (int rk = 0; rk < NRB; ++rk) {
+              const bf16x8 lf = *(const bf16x8*)(Ls + ((i * WAVES_M + wm) * 32 + (lane & 31)) * LP + rk * 16 + (lane >> 5) * 8);
+              const bf16x8 bfr = *(const bf16x8*)(Lb + ((j * WAVES_N + wn) * 32 + (lane & 31)) * LP + rk * 16 + (lane >> 5) * 8);
+              t = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr, lf, t, 0, 0, 0);
+            }
+          }
         }
+        if (row >= mrows) continue;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int n = n0 + (j * WAVES_N + wn) * 32 + 8 * g + col_l;
+          if (n >= p.N) continue;
+          f32x4 bias = {0.f, 0.f, 0.f, 0.f};
+          if (p.bias != nullptr) {
+            const bf16* bp = p.bias + (int64_t)e * p.bias_se + n;
+            bias = f32x4{(float)bp[0], (float)bp[1], (float)bp[2], (float)bp[3]};
+          }
+          float o[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) o[q] = acc[i][j][4 * g + q] * cs[j][g][q] + p.scaling * t[4 * g + q] + bias[q];
+          u32x2 v;
+          v[0] = pack_bf16x2(o[0], o[1]);
+          v[1] = pack_bf16x2(o[2], o[3]);
+          *(u32x2*)(orow + n) = v;
+        }
+      }
     }
   }
 }
 
 // ---- launch ----
 static size_t lds_bytes(int rp, int E) {
-  return (size_t)2 * (BM + BN + rp) * BKP * sizeof(bf16) + (size_t)(2 * (E + 1) + 16) * sizeof(int);
+  return (size_t)2 * (BM + BN + rp) * BK * sizeof(bf16) + (size_t)(2 * (E + 1) + 16) * sizeof(int);
 }
-static_assert(BM * (kMaxRank + 8) + BN * (kMaxRank + 8) <= 2 * BM * BKP, "epilogue views overflow the x stages");
+static_assert(BM * (kMaxRank + 8) <= 2 * BM * BK && BN * (kMaxRank + 8) <= 2 * BN * BK,
+              "the epilogue's low and B^T tiles must fit in the stage buffers they alias");
 
 template <int WDT, bool BKC, bool SCALE_K, int NRB>
 static int launch_t(const GemmArgs& a, hipStream_t s) {
@@ -597,7 +647,7 @@ extern "C" int mlora_grouped_gemm(const void* x, int64_t ldx, int64_t rows, int 
   g.offsets = offsets; g.rows = rows; g.E = E; g.K = K; g.N = N;
   hipStream_t s = as_stream(stream);
   switch (w_dtype) {
-    case MLORA_DT_BF16: return bkc ? launch_r<W_BF16, true, false>(g, s) : launch_r<W_BF16, false, false>(g, s);
+    case MLORA_DT_BF16: return launch_grouped_gemm_bf16(g, bkc, s);
     case MLORA_DT_FP8_E4M3:
       if (scale_k) return bkc ? launch_r<W_FP8, true, true>(g, s) : launch_r<W_FP8, false, true>(g, s);
       return bkc ? launch_r<W_FP8, true, false>(g, s) : launch_r<W_FP8, false, false>(g, s);

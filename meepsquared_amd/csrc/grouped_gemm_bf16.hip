@@ -1,0 +1,421 @@
+// The grouped product for bf16 stacks, fed by LDS DMA through a multi-stage ring (gfx950).
+//
+//   out_e = c · x_e W_e + scaling · bf16(x_e A_e) B_e + bias_e         for every expert e
+//
+// Same work decomposition as the register-staged kernel (grouped_gemm.hip): a persistent grid,
+// each workgroup deriving the tile map in LDS, items split into one contiguous range per XCD.
+// What differs is how operands reach LDS and how deep the pipeline is:
+//   * x tiles, W tiles and A_e^T tiles are copied from HBM/L2 straight into LDS by
+//     buffer_load_dwordx4 ... lds (16 bytes per lane, lane-linear in LDS): no staging registers,
+//     no ds_write, and the copy runs asynchronously behind the MFMAs;
+//   * a ring of STAGES BK-deep stages: the copy of stage kt + STAGES - 1 is issued while stage kt is
+//     multiplied, so each copy has STAGES - 1 iterations of MFMA work to hide its latency; a wave
+//     waits (s_waitcnt vmcnt) only for its own copies of the stage it is about to read, then one
+//     barrier per stage publishes every wave's copies;
+//   * a stack with k contiguous (the forward pass of an (E, out, in) stack) is held as [n][k]; a
+//     stack with n contiguous (the input-gradient pass) is held as it lies in memory, [k][n], and
+//     read with ds_read_b64_tr_b16, which returns each lane four consecutive k of one column: the
+//     MFMA operand, with no transpose pass;
+//   * the global addresses of each DMA lane are chosen so that the lane-linear LDS image is
+//     XOR-swizzled: MFMA operand reads (16 lanes per cycle) hit 16 distinct bank groups.
+// Waves are WAVES_M x WAVES_N; wave (wm, wn) owns the interleaved 32-row blocks i*WAVES_M + wm and
+// 32-column blocks j*WAVES_N + wn; the K loop is specialised on the number of its row blocks that
+// hold rows of the expert (the last tile of an expert is usually partial), with no branch inside.
+//
+// Reference behaviour: src/meepsquared/_grouped.py:120-221 (_grouped_gemm_kernel), :313-345 (_launch).
+#include <mutex>
+#include <unordered_map>
+
+#include "gemm_common.hpp"
+
+namespace mlora {
+namespace dma {
+
+#ifndef MLORA_DMA_WM
+#define MLORA_DMA_WM 2
+#endif
+#ifndef MLORA_DMA_WN
+#define MLORA_DMA_WN 4
+#endif
+#ifndef MLORA_DMA_OCC
+#define MLORA_DMA_OCC 2
+#endif
+
+constexpr int BM = 256, BN = 256, BK = 32, STAGES = 4;
+constexpr int WAVES_M = MLORA_DMA_WM, WAVES_N = MLORA_DMA_WN;
+constexpr int NW = WAVES_M * WAVES_N, kThreads = 64 * NW;
+constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;
+constexpr int FM = WTM / 32, FN = WTN / 32;
+constexpr int kLS = 2 * FM / WAVES_N;          // 16-row halves of x·A_e per wave
+constexpr int XCH = BM * BK / 8, WCH = BN * BK / 8;  // 16-byte chunks per stage
+constexpr int XI = XCH / (64 * NW), WI = WCH / (64 * NW);  // DMA instructions per wave per stage
+static_assert(XCH % (64 * NW) == 0 && WCH % (64 * NW) == 0, "stages must split evenly over the waves");
+static_assert(FM >= 1 && FN >= 1 && (2 * FM) % WAVES_N == 0, "tile shape");
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// [row][k] tiles (rows of BK = 32 bf16, 4 chunks): chunk c of row r in slot c ^ ((r >> 2) & 3)
+__device__ __forceinline__ int swz_rk(int row, int chunk) { return row * BK + ((chunk ^ ((row >> 2) & 3)) << 3); }
+// [k][n] tiles (rows of BN bf16): chunk c of row k in slot c ^ ((k & 3) << 2)
+__device__ __forceinline__ int swz_kn(int k, int chunk) { return k * BN + ((chunk ^ ((k & 3) << 2)) << 3); }
+
+__device__ __forceinline__ void dma16(rsrc_t r, const bf16* lds_dst, uint32_t voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)lds_dst, 16, voff, 0, 0, 0);
+}
+
+// s_waitcnt vmcnt(n) (lgkmcnt and expcnt left free); n is wave-uniform, 0..15
+__device__ __forceinline__ void wait_vm(int n) {
+#define MLORA_W(N) case N: __builtin_amdgcn_s_waitcnt(0x0F70 | N); break;
+  switch (n) {
+    MLORA_W(0) MLORA_W(1) MLORA_W(2) MLORA_W(3) MLORA_W(4) MLORA_W(5) MLORA_W(6) MLORA_W(7)
+    MLORA_W(8) MLORA_W(9) MLORA_W(10) MLORA_W(11) MLORA_W(12) MLORA_W(13) MLORA_W(14)
+    default: __builtin_amdgcn_s_waitcnt(0x0F70 | 15); break;
+  }
+#undef MLORA_W
+}
+
+// A workgroup barrier that waits for nothing but this wave's LDS reads: the DMA copies still in
+// flight stay in flight (a __syncthreads would wait for them all).  The empty asm statements keep
+// the compiler from moving memory accesses across it.
+__device__ __forceinline__ void stage_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+template <bool BKC, int NRB>
+struct Ring {
+  static constexpr int RP = NRB * 16;
+  bf16* As;  // [STAGES][BM * BK]
+  bf16* Bs;  // [STAGES][BN * BK]
+  bf16* Aa;  // [STAGES][RP * BK]
+
+  // Issue the DMA copies of stage kt into slot kt % STAGES.  Returns nothing: every wave issues
+  // XI + WI copies, plus one of A^T when wave < NRB.
+  __device__ __forceinline__ void issue(const GemmArgs& p, rsrc_t rx, rsrc_t rw, rsrc_t ra, int n0, int kt, int wave,
+                                        int lane) const {
+    const int slot = kt % STAGES, k0 = kt * BK;
+    bf16* as = As + slot * BM * BK;
+    bf16* bs = Bs + slot * BN * BK;
+#pragma unroll
+    for (int q = 0; q < XI; ++q) {
+      const int instr = wave * XI + q, ci = instr * 64 + lane;
+      const int row = ci >> 2, c = (ci & 3) ^ ((row >> 2) & 3);
+      const int k = k0 + c * 8;
+      dma16(rx, as + instr * 512, k < p.K ? (uint32_t)((row * p.ldx + k) * 2) : kOob);
+    }
+#pragma unroll
+    for (int q = 0; q < WI; ++q) {
+      const int instr = wave * WI + q, ci = instr * 64 + lane;
+      uint32_t off;
+      if constexpr (BKC) {  // [n][k]
+        const int row = ci >> 2, c = (ci & 3) ^ ((row >> 2) & 3);
+        const int n = n0 + row, k = k0 + c * 8;
+        off = (n < p.N && k < p.K) ? (uint32_t)(((int64_t)n * p.w_sn + k) * 2) : kOob;
+      } else {  // [k][n]
+        const int kr = ci / (BN / 8), c = (ci % (BN / 8)) ^ ((kr & 3) << 2);
+        const int k = k0 + kr, n = n0 + c * 8;
+        off = (k < p.K && n < p.N) ? (uint32_t)(((int64_t)k * p.w_sk + n) * 2) : kOob;
+      }
+      dma16(rw, bs + instr * 512, off);
+    }
+    if constexpr (NRB > 0) {
+      if (wave < NRB) {
+        bf16* aa = Aa + slot * RP * BK;
+        const int ci = wave * 64 + lane;
+        const int r = ci >> 2, c = (ci & 3) ^ ((r >> 2) & 3);
+        const int k = k0 + c * 8;
+        dma16(ra, aa + wave * 512, k < p.K ? (uint32_t)((r * p.at_sr + k) * 2) : kOob);
+      }
+    }
+  }
+};
+
+// the stack's fragment for MFMA (32 columns n at nb, 8 consecutive k at kb + 8*(lane/32))
+template <bool BKC>
+__device__ __forceinline__ bf16x8 w_frag(const bf16* bs, int nb, int kk, int lane) {
+  if constexpr (BKC) {
+    return *(const bf16x8*)(bs + swz_rk(nb + (lane & 31), kk * 2 + (lane >> 5)));
+  } else {
+    // ds_read_b64_tr_b16: in each group of 16 lanes, source lane s points at (k0 + s/4, n0 + 4*(s%4))
+    // and lane i receives the four values (k0 .. k0+3, n0 + i)
+    const int g = lane >> 4, s = lane & 15;
+    const int n = nb + 16 * (g & 1) + 4 * (s & 3);
+    const int k = kk * 16 + 8 * (g >> 1) + (s >> 2);
+    typedef short s16x4 __attribute__((ext_vector_type(4)));
+    const bf16* p0 = bs + swz_kn(k, n >> 3) + (n & 7);
+    const bf16* p1 = bs + swz_kn(k + 4, n >> 3) + (n & 7);
+    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(lds_void*)p0);
+    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(lds_void*)p1);
+    typedef short s16x8 __attribute__((ext_vector_type(8)));
+    const s16x8 v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    return __builtin_bit_cast(bf16x8, v);
+  }
+}
+
+// The K loop of one item for a wave with AM live row blocks; every MFMA unconditional.
+template <int AM, bool BKC, int NRB>
+__device__ __forceinline__ void kloop(const GemmArgs& p, const Ring<BKC, NRB>& ring, rsrc_t rx, rsrc_t rw, rsrc_t ra,
+                                      int n0, int nk, int wave, int lane, int wm, int wn, f32x16 (&acc)[FM][FN],
+                                      f32x4 (&lacc)[kLS][NRB > 0 ? NRB : 1]) {
+  constexpr int RP = NRB * 16;
+  const int per_stage = XI + WI + ((NRB > 0 && wave < NRB) ? 1 : 0);  // this wave's copies per stage
+  for (int kt = 0; kt < nk; ++kt) {
+    // stages kt+1 .. kt+STAGES-2 may stay in flight; stage kt must have landed
+    wait_vm(per_stage * min(STAGES - 2, nk - 1 - kt));
+    stage_barrier();
+    if (kt + STAGES - 1 < nk) ring.issue(p, rx, rw, ra, n0, kt + STAGES - 1, wave, lane);
+    const int slot = kt % STAGES;
+    const bf16* as = ring.As + slot * BM * BK;
+    const bf16* bs = ring.Bs + slot * BN * BK;
+    if constexpr (AM > 0) {
+#pragma unroll
+      for (int kk = 0; kk < BK / 16; ++kk) {
+        bf16x8 af[AM], bfr[FN];
+#pragma unroll
+        for (int i = 0; i < AM; ++i)
+          af[i] = *(const bf16x8*)(as + swz_rk((i * WAVES_M + wm) * 32 + (lane & 31), kk * 2 + (lane >> 5)));
+#pragma unroll
+        for (int j = 0; j < FN; ++j) bfr[j] = w_frag<BKC>(bs, (j * WAVES_N + wn) * 32, kk, lane);
+#pragma unroll
+        for (int i = 0; i < AM; ++i)
+#pragma unroll
+          for (int j = 0; j < FN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[j], af[i], acc[i][j], 0, 0, 0);
+      }
+      if constexpr (NRB > 0) {
+        const bf16* aa = ring.Aa + slot * RP * BK;
+        bf16x8 af[NRB];
+#pragma unroll
+        for (int rb = 0; rb < NRB; ++rb) af[rb] = *(const bf16x8*)(aa + swz_rk(rb * 16 + (lane & 15), lane >> 4));
+#pragma unroll
+        for (int q = 0; q < kLS; ++q) {
+          const int sh = wn + WAVES_N * q;  // this wave's 16-row half: block sh / 2, half sh % 2
+          if ((sh >> 1) < AM) {
+            const int rbase = ((sh >> 1) * WAVES_M + wm) * 32 + (sh & 1) * 16;
+            const bf16x8 xf = *(const bf16x8*)(as + swz_rk(rbase + (lane & 15), lane >> 4));
+#pragma unroll
+            for (int rb = 0; rb < NRB; ++rb)
+              lacc[q][rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf, af[rb], lacc[q][rb], 0, 0, 0);
+          }
+        }
+      }
+    }
+  }
+}
+
+template <bool BKC, int NRB>
+__global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_kernel(GemmArgs p) {
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  constexpr int RP = NRB * 16;
+  constexpr int LP = RP + 8;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+  const int E = p.E;
+
+  Ring<BKC, NRB> ring;
+  ring.As = (bf16*)smem;
+  ring.Bs = ring.As + STAGES * BM * BK;
+  ring.Aa = ring.Bs + STAGES * BN * BK;
+  int* starts = (int*)(ring.Aa + STAGES * RP * BK);
+  int* tstart = starts + (E + 1);
+  bf16* Ls = ring.As;  // epilogue: [BM][LP] and [BN][LP], aliasing the ring once every copy has landed
+  bf16* Lb = ring.Bs;
+
+  build_tile_map<kThreads>(p, BM, starts, tstart, tid);
+  const int nb = (p.N + BN - 1) / BN;
+  const int64_t total = (int64_t)__builtin_amdgcn_readfirstlane(tstart[E]) * nb;
+  const int xcd = blockIdx.x % kXcds, slot = blockIdx.x / kXcds, per_xcd = gridDim.x / kXcds;
+  const int64_t chunk = (total + kXcds - 1) / kXcds;
+  const int64_t beg = xcd * chunk, end = min(beg + chunk, total);
+  const int nk = (p.K + BK - 1) / BK;
+
+  for (int64_t item = beg + slot; item < end; item += per_xcd) {
+    const Item it = decode_item(item, nb, E, BM, BN, starts, tstart);
+    const int e = it.e, n0 = it.n0, mrows = it.mrows;
+    const int64_t row0 = it.row0;
+    const int ncols = min(BN, p.N - n0);
+    const int mb = (mrows + 31) >> 5, nbk = (ncols + 31) >> 5;
+    const int am = min(FM, max(0, (mb - wm + WAVES_M - 1) / WAVES_M));
+    const int an = min(FN, max(0, (nbk - wn + WAVES_N - 1) / WAVES_N));
+
+    const rsrc_t rx = make_rsrc(p.x + row0 * p.ldx, (int64_t)mrows * p.ldx * 2);
+    const rsrc_t rw = make_rsrc(p.w + (int64_t)e * p.w_se * 2, p.w_se * 2);
+    rsrc_t ra = rx;
+    if constexpr (NRB > 0) ra = make_rsrc(p.at + (int64_t)e * p.at_se, (int64_t)RP * p.at_sr * 2);
+
+    f32x16 acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j) acc[i][j] = f32x16{};
+    f32x4 lacc[kLS][NRB > 0 ? NRB : 1];
+#pragma unroll
+    for (int q = 0; q < kLS; ++q)
+#pragma unroll
+      for (int j = 0; j < (NRB > 0 ? NRB : 1); ++j) lacc[q][j] = f32x4{};
+
+    __syncthreads();  // the previous item's epilogue is done with the LDS
+#pragma unroll
+    for (int s = 0; s < STAGES - 1; ++s)
+      if (s < nk) ring.issue(p, rx, rw, ra, n0, s, wave, lane);
+
+    switch (am) {
+      case FM: kloop<FM, BKC, NRB>(p, ring, rx, rw, ra, n0, nk, wave, lane, wm, wn, acc, lacc); break;
+#if (256 / MLORA_DMA_WM / 32) >= 4
+      case 3: kloop<3, BKC, NRB>(p, ring, rx, rw, ra, n0, nk, wave, lane, wm, wn, acc, lacc); break;
+#endif
+#if (256 / MLORA_DMA_WM / 32) >= 3
+      case 2: kloop<2, BKC, NRB>(p, ring, rx, rw, ra, n0, nk, wave, lane, wm, wn, acc, lacc); break;
+#endif
+#if (256 / MLORA_DMA_WM / 32) >= 2
+      case 1: kloop<1, BKC, NRB>(p, ring, rx, rw, ra, n0, nk, wave, lane, wm, wn, acc, lacc); break;
+#endif
+      default: kloop<0, BKC, NRB>(p, ring, rx, rw, ra, n0, nk, wave, lane, wm, wn, acc, lacc); break;
+    }
+    __syncthreads();  // every wave is done with the ring (all copies waited for in the loop)
+
+    // ---- epilogue: as in grouped_gemm.hip ----
+    const int col_l = 4 * (lane >> 5);
+    f32x4 cs[FN][4];
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        if (p.scale_kind == MLORA_SCALE_EXPERT) {
+          const float c = p.scale[e];
+          cs[j][g] = f32x4{c, c, c, c};
+        } else if (p.scale_kind == MLORA_SCALE_ROW) {
+          const int n = n0 + (j * WAVES_N + wn) * 32 + 8 * g + col_l;
+          cs[j][g] = n < p.N ? *(const f32x4*)(p.scale + (int64_t)e * p.scale_se + n) : f32x4{};
+        } else {
+          cs[j][g] = f32x4{1.f, 1.f, 1.f, 1.f};
+        }
+      }
+    if constexpr (NRB > 0) {
+#pragma unroll
+      for (int q = 0; q < kLS; ++q) {
+        const int sh = wn + WAVES_N * q;
+        const int rbase = ((sh >> 1) * WAVES_M + wm) * 32 + (sh & 1) * 16;
+#pragma unroll
+        for (int rb = 0; rb < NRB; ++rb)
+#pragma unroll
+          for (int v = 0; v < 4; ++v)
+            Ls[(rbase + 4 * (lane >> 4) + v) * LP + rb * 16 + (lane & 15)] = (bf16)lacc[q][rb][v];
+      }
+      const rsrc_t rbt = make_rsrc(p.bt + (int64_t)e * p.bt_se, (int64_t)p.N * p.bt_sn * 2);
+      for (int c = tid; c < BN * RP / 8; c += kThreads) {
+        const int nn = c / (RP / 8), rc = (c - nn * (RP / 8)) * 8;
+        const int n = n0 + nn;
+        *(u32x4*)(Lb + nn * LP + rc) = ld128(rbt, n < p.N ? (uint32_t)((n * p.bt_sn + rc) * 2) : kOob);
+      }
+      __syncthreads();
+      if (p.low != nullptr && it.nblk == 0) {
+        for (int c = tid; c < BM * RP / 8; c += kThreads) {
+          const int m = c / (RP / 8), rc = (c - m * (RP / 8)) * 8;
+          if (m < mrows) *(u32x4*)(p.low + (row0 + m) * p.ldl + rc) = *(const u32x4*)(Ls + m * LP + rc);
+        }
+      }
+    }
+    const bool lora_on = NRB > 0 && p.scaling != 0.f;
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      const int row = (i * WAVES_M + wm) * 32 + (lane & 31);
+      if (i >= am) continue;
+      bf16* orow = p.out + (row0 + row) * p.ldo;
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        if (j >= an) continue;
+        f32x16 t = f32x16{};
+        if constexpr (NRB > 0) {
+          if (lora_on) {
+#pragma unroll
+            for (int rk = 0; rk < NRB; ++rk) {
+              const bf16x8 lf = *(const bf16x8*)(Ls + ((i * WAVES_M + wm) * 32 + (lane & 31)) * LP + rk * 16 + (lane >> 5) * 8);
+              const bf16x8 bfr = *(const bf16x8*)(Lb + ((j * WAVES_N + wn) * 32 + (lane & 31)) * LP + rk * 16 + (lane >> 5) * 8);
+              t = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr, lf, t, 0, 0, 0);
+            }
+          }
+        }
+        if (row >= mrows) continue;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int n = n0 + (j * WAVES_N + wn) * 32 + 8 * g + col_l;
+          if (n >= p.N) continue;
+          f32x4 bias = {0.f, 0.f, 0.f, 0.f};
+          if (p.bias != nullptr) {
+            const bf16* bp = p.bias + (int64_t)e * p.bias_se + n;
+            bias = f32x4{(float)bp[0], (float)bp[1], (float)bp[2], (float)bp[3]};
+          }
+          float o[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) o[q] = acc[i][j][4 * g + q] * cs[j][g][q] + p.scaling * t[4 * g + q] + bias[q];
+          u32x2 v;
+          v[0] = pack_bf16x2(o[0], o[1]);
+          v[1] = pack_bf16x2(o[2], o[3]);
+          *(u32x2*)(orow + n) = v;
+        }
+      }
+    }
+  }
+}
+
+static size_t lds_bytes(int rp, int E) {
+  return (size_t)STAGES * (BM + BN + rp) * BK * sizeof(bf16) + (size_t)(2 * (E + 1)) * sizeof(int);
+}
+static_assert(BM * (kMaxRank + 8) <= STAGES * BM * BK && BN * (kMaxRank + 8) <= STAGES * BN * BK,
+              "the epilogue's low and B^T tiles must fit in the ring they alias");
+
+template <bool BKC, int NRB>
+static int launch_t(const GemmArgs& a, hipStream_t s) {
+  auto kern = grouped_gemm_bf16_kernel<BKC, NRB>;
+  const size_t lds = lds_bytes(NRB * 16, a.E);
+  static std::mutex mu;
+  static std::unordered_map<int64_t, int> grid_cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return fail("grouped_gemm: hipGetDevice failed");
+  int grid = 0;
+  {
+    std::lock_guard<std::mutex> g(mu);
+    const int64_t key = ((int64_t)dev << 32) | (int64_t)lds;
+    auto it = grid_cache.find(key);
+    if (it != grid_cache.end()) {
+      grid = it->second;
+    } else {
+      if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+        return fail("grouped_gemm: cannot grant %zu bytes of LDS", lds);
+      int cus = 0, per_cu = 0;
+      if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
+        return fail("grouped_gemm: cannot read the compute unit count");
+      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void*)kern, kThreads, lds) != hipSuccess ||
+          per_cu < 1)
+        per_cu = 1;
+      grid = (cus * per_cu + kXcds - 1) / kXcds * kXcds;
+      grid_cache[key] = grid;
+    }
+  }
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(kThreads), lds, s, a);
+  return launch_status("grouped_gemm");
+}
+
+template <bool BKC>
+static int launch_r(const GemmArgs& a, hipStream_t s) {
+  switch (a.rank / 16) {
+    case 0: return launch_t<BKC, 0>(a, s);
+    case 1: return launch_t<BKC, 1>(a, s);
+    case 2: return launch_t<BKC, 2>(a, s);
+    case 3: return launch_t<BKC, 3>(a, s);
+    default: return launch_t<BKC, 4>(a, s);
+  }
+}
+
+}  // namespace dma
+
+int launch_grouped_gemm_bf16(const GemmArgs& a, bool k_contiguous, hipStream_t s) {
+  if (a.scale_kind == MLORA_SCALE_ROW && a.scale_se == 0) return fail("grouped_gemm: per-row scale without a stride");
+  return k_contiguous ? dma::launch_r<true>(a, s) : dma::launch_r<false>(a, s);
+}
+
+}  // namespace mlora
