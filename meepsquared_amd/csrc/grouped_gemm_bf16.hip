@@ -38,7 +38,7 @@ namespace dma {
 #define MLORA_DMA_WN 4
 #endif
 #ifndef MLORA_DMA_OCC
-#define MLORA_DMA_OCC 2
+#define MLORA_DMA_OCC 1
 #endif
 
 constexpr int BM = 256, BN = 256, BK = 32, STAGES = 4;
@@ -63,15 +63,11 @@ __device__ __forceinline__ void dma16(rsrc_t r, const bf16* lds_dst, uint32_t vo
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)lds_dst, 16, voff, 0, 0, 0);
 }
 
-// s_waitcnt vmcnt(n) (lgkmcnt and expcnt left free); n is wave-uniform, 0..15
-__device__ __forceinline__ void wait_vm(int n) {
-#define MLORA_W(N) case N: __builtin_amdgcn_s_waitcnt(0x0F70 | N); break;
-  switch (n) {
-    MLORA_W(0) MLORA_W(1) MLORA_W(2) MLORA_W(3) MLORA_W(4) MLORA_W(5) MLORA_W(6) MLORA_W(7)
-    MLORA_W(8) MLORA_W(9) MLORA_W(10) MLORA_W(11) MLORA_W(12) MLORA_W(13) MLORA_W(14)
-    default: __builtin_amdgcn_s_waitcnt(0x0F70 | 15); break;
-  }
-#undef MLORA_W
+// s_waitcnt vmcnt(N) with expcnt and lgkmcnt left free
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
 }
 
 // A workgroup barrier that waits for nothing but this wave's LDS reads: the DMA copies still in
@@ -84,50 +80,136 @@ __device__ __forceinline__ void stage_barrier() {
   asm volatile("" ::: "memory");
 }
 
-template <bool BKC, int NRB>
-struct Ring {
-  static constexpr int RP = NRB * 16;
-  bf16* As;  // [STAGES][BM * BK]
-  bf16* Bs;  // [STAGES][BN * BK]
-  bf16* Aa;  // [STAGES][RP * BK]
+// The tile map in LDS, one int per expert: tend[e] = the number of BM-row tiles of experts 0..e
+// (an inclusive scan; tend[E-1] is the tile count).  Expert e's rows are [start(e), start(e+1)) with
+// start(e) = offsets[e-1] clamped into [0, rows] (start(0) = 0), read from global memory when needed.
+__device__ __forceinline__ int64_t row_start(const GemmArgs& p, int e) {
+  if (e == 0) return 0;
+  const int64_t o = p.offsets[e - 1];
+  return o < 0 ? 0 : (o > p.rows ? p.rows : o);
+}
 
-  // Issue the DMA copies of stage kt into slot kt % STAGES.  Returns nothing: every wave issues
-  // XI + WI copies, plus one of A^T when wave < NRB.
-  __device__ __forceinline__ void issue(const GemmArgs& p, rsrc_t rx, rsrc_t rw, rsrc_t ra, int n0, int kt, int wave,
-                                        int lane) const {
-    const int slot = kt % STAGES, k0 = kt * BK;
-    bf16* as = As + slot * BM * BK;
-    bf16* bs = Bs + slot * BN * BK;
+__device__ __forceinline__ void build_tile_ends(const GemmArgs& p, int* tend, int tid) {
+  const int E = p.E;
+  for (int e = tid; e < E; e += kThreads) {
+    const int64_t c = row_start(p, e + 1) - row_start(p, e);
+    tend[e] = c > 0 ? (int)((c + BM - 1) / BM) : 0;
+  }
+  __syncthreads();
+  if (tid < 64) {  // inclusive scan by one wave, 64 experts at a time
+    const int lane = tid;
+    int run = 0;
+    for (int base = 0; base < E; base += 64) {
+      const int e = base + lane;
+      int incl = e < E ? tend[e] : 0;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int u = __shfl_up(incl, o, 64);
+        if (lane >= o) incl += u;
+      }
+      if (e < E) tend[e] = run + incl;
+      run += __shfl(incl, 63, 64);
+    }
+  }
+  __syncthreads();
+}
+
+// work item (tile t, column block) -> wave-uniform expert, rows and columns
+__device__ __forceinline__ Item decode(const GemmArgs& p, int64_t item, int nb, const int* tend) {
+  const int t = (int)(item / nb);
+  Item it;
+  it.nblk = (int)(item - (int64_t)t * nb);
+  int lo = 0, hi = p.E - 1;  // the expert e with tend[e-1] <= t < tend[e]
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    if (tend[mid] > t) hi = mid; else lo = mid + 1;
+  }
+  it.e = __builtin_amdgcn_readfirstlane(lo);
+  const int t0 = it.e == 0 ? 0 : __builtin_amdgcn_readfirstlane(tend[it.e - 1]);
+  it.row0 = row_start(p, it.e) + (int64_t)(t - t0) * BM;
+  it.mrows = (int)min((int64_t)BM, row_start(p, it.e + 1) - it.row0);
+  it.n0 = it.nblk * BN;
+  return it;
+}
+
+// One ring slot: the x tile [BM][BK], the stack tile ([BN][BK] or [BK][BN]) and the A_e^T tile
+// [RP][BK].  Each slot is its own LDS object, so the compiler can tell a read of one slot from the
+// copies still landing in the others and does not wait for those.
+// The A^T tile is copied with RD rows: the rank padded so that the copies split over the eight
+// waves in whole runs of lanes (rank 48 is copied as 64 rows, the last 16 read as zeros).
+template <int NRB>
+struct SlotSize {
+  static constexpr int RD = (NRB == 3 ? 4 : NRB) * 16;
+  static constexpr int kElems = (BM + BN + RD) * BK;
+};
+
+// Per-lane DMA addressing of one item, fixed for its whole K loop: byte offsets at k = 0 and the
+// k of each lane's chunk (a huge k marks a column past N: never in range).
+template <bool BKC, int NRB>
+struct Feed {
+  static constexpr int RP = NRB * 16;
+  static constexpr int CPW = SlotSize<NRB>::RD * BK / 8 / NW;  // A^T chunks per wave per stage
+  static_assert(NRB == 0 || (CPW > 0 && 64 % CPW == 0), "each wave's A^T chunks lie in one 64-lane copy");
+  // this wave's copies per stage: XI of x, WI of the stack, one (lane-masked) of A^T
+  static constexpr int PS = XI + WI + (NRB > 0 ? 1 : 0);
+  rsrc_t rx, rw, ra;
+  uint32_t xo[XI], wo[WI], ao;
+  int xk[XI], wk[WI], ak;
+  int xd[XI], wd[WI], ad;  // LDS element offset of each instruction's 64 lanes within the slot
+  bool a_on;
+  int64_t wstep;           // bytes the stack offset advances per k (BKC: 2; else 2 * w_sk)
+
+  __device__ __forceinline__ void init(const GemmArgs& p, int n0, int wave, int lane) {
 #pragma unroll
     for (int q = 0; q < XI; ++q) {
       const int instr = wave * XI + q, ci = instr * 64 + lane;
       const int row = ci >> 2, c = (ci & 3) ^ ((row >> 2) & 3);
-      const int k = k0 + c * 8;
-      dma16(rx, as + instr * 512, k < p.K ? (uint32_t)((row * p.ldx + k) * 2) : kOob);
+      xo[q] = (uint32_t)((row * p.ldx + c * 8) * 2);
+      xk[q] = c * 8;
+      xd[q] = instr * 512;
     }
 #pragma unroll
     for (int q = 0; q < WI; ++q) {
       const int instr = wave * WI + q, ci = instr * 64 + lane;
-      uint32_t off;
       if constexpr (BKC) {  // [n][k]
         const int row = ci >> 2, c = (ci & 3) ^ ((row >> 2) & 3);
-        const int n = n0 + row, k = k0 + c * 8;
-        off = (n < p.N && k < p.K) ? (uint32_t)(((int64_t)n * p.w_sn + k) * 2) : kOob;
+        const int n = n0 + row;
+        wo[q] = n < p.N ? (uint32_t)(((int64_t)n * p.w_sn + c * 8) * 2) : 0u;
+        wk[q] = n < p.N ? c * 8 : (1 << 30);
       } else {  // [k][n]
         const int kr = ci / (BN / 8), c = (ci % (BN / 8)) ^ ((kr & 3) << 2);
-        const int k = k0 + kr, n = n0 + c * 8;
-        off = (k < p.K && n < p.N) ? (uint32_t)(((int64_t)k * p.w_sk + n) * 2) : kOob;
+        const int n = n0 + c * 8;
+        wo[q] = n < p.N ? (uint32_t)(((int64_t)kr * p.w_sk + n) * 2) : 0u;
+        wk[q] = n < p.N ? kr : (1 << 30);
       }
-      dma16(rw, bs + instr * 512, off);
+      wd[q] = BM * BK + instr * 512;
     }
+    wstep = BKC ? 2 : 2 * p.w_sk;
     if constexpr (NRB > 0) {
-      if (wave < NRB) {
-        bf16* aa = Aa + slot * RP * BK;
-        const int ci = wave * 64 + lane;
-        const int r = ci >> 2, c = (ci & 3) ^ ((r >> 2) & 3);
-        const int k = k0 + c * 8;
-        dma16(ra, aa + wave * 512, k < p.K ? (uint32_t)((r * p.at_sr + k) * 2) : kOob);
-      }
+      // wave w copies chunks [w * CPW, (w + 1) * CPW) of the A^T tile: lanes of one 64-chunk
+      // instruction block, the others masked off (their LDS bytes belong to other waves)
+      const int c0 = wave * CPW, blk = c0 >> 6;
+      const int ci = blk * 64 + lane;
+      const int r = ci >> 2, c = (ci & 3) ^ ((r >> 2) & 3);
+      ao = (uint32_t)((r * p.at_sr + c * 8) * 2);
+      ak = c * 8;
+      ad = (BM + BN) * BK + blk * 512;
+      a_on = lane >= (c0 & 63) && lane < (c0 & 63) + CPW;
+    }
+  }
+
+  // the copies of stage kt into `slot` (past the end of K they read zeros, so the count per stage
+  // never changes)
+  __device__ __forceinline__ void issue(const GemmArgs& p, bf16* slot, int kt) const {
+    const int k0 = kt * BK;
+#pragma unroll
+    for (int q = 0; q < XI; ++q)
+      dma16(rx, slot + xd[q], xk[q] + k0 < p.K ? xo[q] + (uint32_t)(k0 * 2) : kOob);
+#pragma unroll
+    for (int q = 0; q < WI; ++q)
+      dma16(rw, slot + wd[q], wk[q] + k0 < p.K ? wo[q] + (uint32_t)(k0 * wstep) : kOob);
+    if constexpr (NRB > 0) {
+      if (a_on) dma16(ra, slot + ad, ak + k0 < p.K ? ao + (uint32_t)(k0 * 2) : kOob);
     }
   }
 };
@@ -154,86 +236,107 @@ __device__ __forceinline__ bf16x8 w_frag(const bf16* bs, int nb, int kk, int lan
   }
 }
 
-// The K loop of one item for a wave with AM live row blocks; every MFMA unconditional.
+// The MFMAs of one stage held in `slot` for a wave with AM live row blocks.
 template <int AM, bool BKC, int NRB>
-__device__ __forceinline__ void kloop(const GemmArgs& p, const Ring<BKC, NRB>& ring, rsrc_t rx, rsrc_t rw, rsrc_t ra,
-                                      int n0, int nk, int wave, int lane, int wm, int wn, f32x16 (&acc)[FM][FN],
-                                      f32x4 (&lacc)[kLS][NRB > 0 ? NRB : 1]) {
-  constexpr int RP = NRB * 16;
-  const int per_stage = XI + WI + ((NRB > 0 && wave < NRB) ? 1 : 0);  // this wave's copies per stage
-  for (int kt = 0; kt < nk; ++kt) {
-    // stages kt+1 .. kt+STAGES-2 may stay in flight; stage kt must have landed
-    wait_vm(per_stage * min(STAGES - 2, nk - 1 - kt));
-    stage_barrier();
-    if (kt + STAGES - 1 < nk) ring.issue(p, rx, rw, ra, n0, kt + STAGES - 1, wave, lane);
-    const int slot = kt % STAGES;
-    const bf16* as = ring.As + slot * BM * BK;
-    const bf16* bs = ring.Bs + slot * BN * BK;
-    if constexpr (AM > 0) {
+__device__ __forceinline__ void compute(const bf16* slot, int lane, int wm, int wn, f32x16 (&acc)[FM][FN],
+                                        f32x4 (&lacc)[kLS][NRB > 0 ? NRB : 1]) {
+  const bf16* as = slot;
+  const bf16* bs = slot + BM * BK;
+  if constexpr (AM > 0) {
 #pragma unroll
-      for (int kk = 0; kk < BK / 16; ++kk) {
-        bf16x8 af[AM], bfr[FN];
+    for (int kk = 0; kk < BK / 16; ++kk) {
+      bf16x8 af[AM], bfr[FN];
 #pragma unroll
-        for (int i = 0; i < AM; ++i)
-          af[i] = *(const bf16x8*)(as + swz_rk((i * WAVES_M + wm) * 32 + (lane & 31), kk * 2 + (lane >> 5)));
+      for (int i = 0; i < AM; ++i)
+        af[i] = *(const bf16x8*)(as + swz_rk((i * WAVES_M + wm) * 32 + (lane & 31), kk * 2 + (lane >> 5)));
 #pragma unroll
-        for (int j = 0; j < FN; ++j) bfr[j] = w_frag<BKC>(bs, (j * WAVES_N + wn) * 32, kk, lane);
+      for (int j = 0; j < FN; ++j) bfr[j] = w_frag<BKC>(bs, (j * WAVES_N + wn) * 32, kk, lane);
 #pragma unroll
-        for (int i = 0; i < AM; ++i)
+      for (int i = 0; i < AM; ++i)
 #pragma unroll
-          for (int j = 0; j < FN; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[j], af[i], acc[i][j], 0, 0, 0);
-      }
-      if constexpr (NRB > 0) {
-        const bf16* aa = ring.Aa + slot * RP * BK;
-        bf16x8 af[NRB];
+        for (int j = 0; j < FN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[j], af[i], acc[i][j], 0, 0, 0);
+    }
+    if constexpr (NRB > 0) {
+      const bf16* aa = slot + (BM + BN) * BK;
+      bf16x8 ar[NRB];
 #pragma unroll
-        for (int rb = 0; rb < NRB; ++rb) af[rb] = *(const bf16x8*)(aa + swz_rk(rb * 16 + (lane & 15), lane >> 4));
+      for (int rb = 0; rb < NRB; ++rb) ar[rb] = *(const bf16x8*)(aa + swz_rk(rb * 16 + (lane & 15), lane >> 4));
 #pragma unroll
-        for (int q = 0; q < kLS; ++q) {
-          const int sh = wn + WAVES_N * q;  // this wave's 16-row half: block sh / 2, half sh % 2
-          if ((sh >> 1) < AM) {
-            const int rbase = ((sh >> 1) * WAVES_M + wm) * 32 + (sh & 1) * 16;
-            const bf16x8 xf = *(const bf16x8*)(as + swz_rk(rbase + (lane & 15), lane >> 4));
+      for (int q = 0; q < kLS; ++q) {
+        const int sh = wn + WAVES_N * q;  // this wave's 16-row half: block sh / 2, half sh % 2
+        if ((sh >> 1) < AM) {
+          const int rbase = ((sh >> 1) * WAVES_M + wm) * 32 + (sh & 1) * 16;
+          const bf16x8 xf = *(const bf16x8*)(as + swz_rk(rbase + (lane & 15), lane >> 4));
 #pragma unroll
-            for (int rb = 0; rb < NRB; ++rb)
-              lacc[q][rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf, af[rb], lacc[q][rb], 0, 0, 0);
-          }
+          for (int rb = 0; rb < NRB; ++rb)
+            lacc[q][rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf, ar[rb], lacc[q][rb], 0, 0, 0);
         }
       }
     }
   }
 }
 
+// One iteration of the K loop: wait for this wave's copies of stage kt (slot S), publish every
+// wave's with a barrier, queue stage kt + STAGES - 1 into the slot read one iteration ago, multiply.
+template <int S, int AM, bool BKC, int NRB>
+__device__ __forceinline__ void stage(const GemmArgs& p, const Feed<BKC, NRB>& f, bf16* const (&slots)[STAGES], int kt,
+                                      int lane, int wm, int wn, f32x16 (&acc)[FM][FN],
+                                      f32x4 (&lacc)[kLS][NRB > 0 ? NRB : 1]) {
+  wait_vm<Feed<BKC, NRB>::PS * (STAGES - 2)>();  // stages kt+1, kt+2 may stay in flight
+  stage_barrier();
+  f.issue(p, slots[(S + STAGES - 1) % STAGES], kt + STAGES - 1);
+  compute<AM, BKC, NRB>(slots[S], lane, wm, wn, acc, lacc);
+}
+
+// The K loop of one item, unrolled by the ring depth so every slot index is a constant.
+template <int AM, bool BKC, int NRB>
+__device__ __forceinline__ void kloop(const GemmArgs& p, const Feed<BKC, NRB>& f, bf16* const (&slots)[STAGES], int nk,
+                                      int lane, int wm, int wn, f32x16 (&acc)[FM][FN],
+                                      f32x4 (&lacc)[kLS][NRB > 0 ? NRB : 1]) {
+  static_assert(STAGES == 4, "the unrolled loop below is written for four slots");
+  int kt = 0;
+  for (; kt + STAGES <= nk; kt += STAGES) {
+    stage<0, AM, BKC, NRB>(p, f, slots, kt, lane, wm, wn, acc, lacc);
+    stage<1, AM, BKC, NRB>(p, f, slots, kt + 1, lane, wm, wn, acc, lacc);
+    stage<2, AM, BKC, NRB>(p, f, slots, kt + 2, lane, wm, wn, acc, lacc);
+    stage<3, AM, BKC, NRB>(p, f, slots, kt + 3, lane, wm, wn, acc, lacc);
+  }
+  const int rem = nk - kt;  // 0 .. 3 stages left
+  if (rem > 0) stage<0, AM, BKC, NRB>(p, f, slots, kt, lane, wm, wn, acc, lacc);
+  if (rem > 1) stage<1, AM, BKC, NRB>(p, f, slots, kt + 1, lane, wm, wn, acc, lacc);
+  if (rem > 2) stage<2, AM, BKC, NRB>(p, f, slots, kt + 2, lane, wm, wn, acc, lacc);
+}
+
 template <bool BKC, int NRB>
 __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_kernel(GemmArgs p) {
-  extern __shared__ __attribute__((aligned(16))) char smem[];
   constexpr int RP = NRB * 16;
   constexpr int LP = RP + 8;
+  constexpr int SE = SlotSize<NRB>::kElems;
+  __shared__ __attribute__((aligned(16))) bf16 slot0[SE];
+  __shared__ __attribute__((aligned(16))) bf16 slot1[SE];
+  __shared__ __attribute__((aligned(16))) bf16 slot2[SE];
+  __shared__ __attribute__((aligned(16))) bf16 slot3[SE];
+  extern __shared__ __attribute__((aligned(16))) int tile_map[];
+  bf16* const slots[STAGES] = {slot0, slot1, slot2, slot3};
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WAVES_N, wn = wave % WAVES_N;
   const int E = p.E;
 
-  Ring<BKC, NRB> ring;
-  ring.As = (bf16*)smem;
-  ring.Bs = ring.As + STAGES * BM * BK;
-  ring.Aa = ring.Bs + STAGES * BN * BK;
-  int* starts = (int*)(ring.Aa + STAGES * RP * BK);
-  int* tstart = starts + (E + 1);
-  bf16* Ls = ring.As;  // epilogue: [BM][LP] and [BN][LP], aliasing the ring once every copy has landed
-  bf16* Lb = ring.Bs;
+  bf16* Ls = slot0;  // epilogue: [BM][LP] and [BN][LP], in slots the ring has finished with
+  bf16* Lb = slot1;
 
-  build_tile_map<kThreads>(p, BM, starts, tstart, tid);
+  build_tile_ends(p, tile_map, tid);
   const int nb = (p.N + BN - 1) / BN;
-  const int64_t total = (int64_t)__builtin_amdgcn_readfirstlane(tstart[E]) * nb;
-  const int xcd = blockIdx.x % kXcds, slot = blockIdx.x / kXcds, per_xcd = gridDim.x / kXcds;
+  const int64_t total = (int64_t)__builtin_amdgcn_readfirstlane(tile_map[E - 1]) * nb;
+  const int xcd = blockIdx.x % kXcds, wg_slot = blockIdx.x / kXcds, per_xcd = gridDim.x / kXcds;
   const int64_t chunk = (total + kXcds - 1) / kXcds;
   const int64_t beg = xcd * chunk, end = min(beg + chunk, total);
   const int nk = (p.K + BK - 1) / BK;
 
-  for (int64_t item = beg + slot; item < end; item += per_xcd) {
-    const Item it = decode_item(item, nb, E, BM, BN, starts, tstart);
+  for (int64_t item = beg + wg_slot; item < end; item += per_xcd) {
+    const Item it = decode(p, item, nb, tile_map);
     const int e = it.e, n0 = it.n0, mrows = it.mrows;
     const int64_t row0 = it.row0;
     const int ncols = min(BN, p.N - n0);
@@ -241,10 +344,12 @@ __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_ker
     const int am = min(FM, max(0, (mb - wm + WAVES_M - 1) / WAVES_M));
     const int an = min(FN, max(0, (nbk - wn + WAVES_N - 1) / WAVES_N));
 
-    const rsrc_t rx = make_rsrc(p.x + row0 * p.ldx, (int64_t)mrows * p.ldx * 2);
-    const rsrc_t rw = make_rsrc(p.w + (int64_t)e * p.w_se * 2, p.w_se * 2);
-    rsrc_t ra = rx;
-    if constexpr (NRB > 0) ra = make_rsrc(p.at + (int64_t)e * p.at_se, (int64_t)RP * p.at_sr * 2);
+    Feed<BKC, NRB> f;
+    f.rx = make_rsrc(p.x + row0 * p.ldx, (int64_t)mrows * p.ldx * 2);
+    f.rw = make_rsrc(p.w + (int64_t)e * p.w_se * 2, p.w_se * 2);
+    f.ra = f.rx;
+    if constexpr (NRB > 0) f.ra = make_rsrc(p.at + (int64_t)e * p.at_se, (int64_t)RP * p.at_sr * 2);
+    f.init(p, n0, wave, lane);
 
     f32x16 acc[FM][FN];
 #pragma unroll
@@ -259,22 +364,22 @@ __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_ker
 
     __syncthreads();  // the previous item's epilogue is done with the LDS
 #pragma unroll
-    for (int s = 0; s < STAGES - 1; ++s)
-      if (s < nk) ring.issue(p, rx, rw, ra, n0, s, wave, lane);
+    for (int s = 0; s < STAGES - 1; ++s) f.issue(p, slots[s], s);
 
     switch (am) {
-      case FM: kloop<FM, BKC, NRB>(p, ring, rx, rw, ra, n0, nk, wave, lane, wm, wn, acc, lacc); break;
+      case FM: kloop<FM, BKC, NRB>(p, f, slots, nk, lane, wm, wn, acc, lacc); break;
 #if (256 / MLORA_DMA_WM / 32) >= 4
-      case 3: kloop<3, BKC, NRB>(p, ring, rx, rw, ra, n0, nk, wave, lane, wm, wn, acc, lacc); break;
+      case 3: kloop<3, BKC, NRB>(p, f, slots, nk, lane, wm, wn, acc, lacc); break;
 #endif
 #if (256 / MLORA_DMA_WM / 32) >= 3
-      case 2: kloop<2, BKC, NRB>(p, ring, rx, rw, ra, n0, nk, wave, lane, wm, wn, acc, lacc); break;
+      case 2: kloop<2, BKC, NRB>(p, f, slots, nk, lane, wm, wn, acc, lacc); break;
 #endif
 #if (256 / MLORA_DMA_WM / 32) >= 2
-      case 1: kloop<1, BKC, NRB>(p, ring, rx, rw, ra, n0, nk, wave, lane, wm, wn, acc, lacc); break;
+      case 1: kloop<1, BKC, NRB>(p, f, slots, nk, lane, wm, wn, acc, lacc); break;
 #endif
-      default: kloop<0, BKC, NRB>(p, ring, rx, rw, ra, n0, nk, wave, lane, wm, wn, acc, lacc); break;
+      default: kloop<0, BKC, NRB>(p, f, slots, nk, lane, wm, wn, acc, lacc); break;
     }
+    wait_vm<0>();     // the zero-filled copies queued past the end of K
     __syncthreads();  // every wave is done with the ring (all copies waited for in the loop)
 
     // ---- epilogue: as in grouped_gemm.hip ----
@@ -362,16 +467,15 @@ __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_ker
   }
 }
 
-static size_t lds_bytes(int rp, int E) {
-  return (size_t)STAGES * (BM + BN + rp) * BK * sizeof(bf16) + (size_t)(2 * (E + 1)) * sizeof(int);
-}
-static_assert(BM * (kMaxRank + 8) <= STAGES * BM * BK && BN * (kMaxRank + 8) <= STAGES * BN * BK,
-              "the epilogue's low and B^T tiles must fit in the ring they alias");
+static size_t lds_bytes(int E) { return (size_t)E * sizeof(int); }
+static_assert(BM * (kMaxRank + 8) <= SlotSize<4>::kElems && BN * (kMaxRank + 8) <= SlotSize<4>::kElems,
+              "the epilogue's low and B^T tiles must fit in the slots they reuse");
+static_assert(4 * SlotSize<4>::kElems * 2 + 4096 * 4 <= 163840, "four slots and the largest tile map fit in LDS");
 
 template <bool BKC, int NRB>
 static int launch_t(const GemmArgs& a, hipStream_t s) {
   auto kern = grouped_gemm_bf16_kernel<BKC, NRB>;
-  const size_t lds = lds_bytes(NRB * 16, a.E);
+  const size_t lds = lds_bytes(a.E);
   static std::mutex mu;
   static std::unordered_map<int64_t, int> grid_cache;
   int dev = 0;
