@@ -1,6 +1,7 @@
 """MoE-LoRA layer forward + backward throughput on one MI355X: BASELINE config 1 (Qwen3-30B-A3B shaped).
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline]
+    python bench.py --copy-calibration MIB    # a plain device copy of known size, for PMC scaling
 
 A step is one forward and backward pass of the routed MoE-LoRA layer over one batch of synthetic
 inputs already resident in HBM: router top-k softmax (from given logits), counting sort, gather,
@@ -118,6 +119,21 @@ def read_traffic():
     return None
 
 
+def copy_calibration(mib: int, reps: int = 3):
+    """Copy a buffer of `mib` MiB device to device `reps` times: under rocprofv3 --pmc, FETCH_SIZE and
+    WRITE_SIZE of these dispatches against the known byte count give the counters' scale factor."""
+    import torch
+
+    n = mib << 20
+    src = torch.empty(n, dtype=torch.uint8, device="cuda:0").fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_per_dispatch": n, "dispatches": reps}))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -125,10 +141,14 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--cpu-tokens", type=int, default=T)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {a.gpus})", file=sys.stderr)
         sys.exit(2)
+    if a.copy_calibration:
+        copy_calibration(a.copy_calibration)
+        return
 
     import torch
 
@@ -207,7 +227,7 @@ def main():
                    "lora_rank": R, "lora_alpha": ALPHA, "parallelism": "single GPU"},
         "step_tflops": round(flops / (ms_per_step / 1e3) / 1e12, 2),
         "step_frac_of_bf16_peak": round(flops / (ms_per_step / 1e3) / 1e12 / PEAK_BF16_TFLOPS, 4),
-        "roofline": {"bound": "mfma", "kernel": "grouped_gemm_kernel (4 launches per step)",
+        "roofline": {"bound": "mfma", "kernel": "grouped_gemm_bf16_kernel (4 launches per step; traffic = mean HBM bytes per launch, rocprofv3 PMC)",
                      "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": read_traffic()},
         "kernel_ms_per_step": {"grouped_gemm": round(gemm_ms / a.steps, 4),
