@@ -161,6 +161,12 @@ int mlora_combine_backward(const void* dout, const void* y, int64_t H, const voi
                            const int64_t* inv, int64_t T, int k, const int32_t* offsets, int E,
                            void* dy, void* dw, void* stream);
 
+/* dst[e][b][a] = src[e*s_e + a*s_a + b*s_b] (bf16): a batched transpose into a contiguous (E, B, A)
+ * tensor, for the adapters' roles in the input-gradient product, which
+ * src/meepsquared/_grouped.py:304-310 (_Adapters.swapped) addresses by strides. */
+int mlora_transpose(const void* src, int64_t E, int64_t A, int64_t B, int64_t s_e, int64_t s_a, int64_t s_b,
+                    void* dst, void* stream);
+
 /* ---------------------------------------------------------------------------------------------
  * Frozen stack formats
  * ------------------------------------------------------------------------------------------- */

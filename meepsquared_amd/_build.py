@@ -1,6 +1,9 @@
 """Builds libmlora.so, the HIP kernels of this package, for gfx950 with hipcc, in the source tree.
 
-    python -m meepsquared_amd._build [--jobs N]
+    python meepsquared_amd/_build.py [--jobs N]
+
+(run by its path: `python -m meepsquared_amd._build` would import the package first, and the
+package loads the library this script is about to rebuild).
 
 Each `csrc/*.hip` file is compiled to an object in `csrc/_objs/` (in parallel) and the objects are
 linked into `meepsquared_amd/_lib/libmlora.so`, which `meepsquared_amd._lib` loads.  Every call

@@ -121,9 +121,17 @@ class _Adapters:
         """The adapters of the input-gradient product: B takes A's role and A B's (_grouped.py:304-310)."""
         other = object.__new__(_Adapters)
         other.rank, other.padded = self.rank, self.padded
-        other.at = self.bt.transpose(1, 2).contiguous()  # (e, R, n): B's rows become the new k
-        other.bt = self.at.transpose(1, 2).contiguous()  # (e, k, R)
+        other.at = _transposed(self.bt)  # (e, R, n): B's rows become the new k
+        other.bt = _transposed(self.at)  # (e, k, R)
         return other
+
+
+def _transposed(t: torch.Tensor) -> torch.Tensor:
+    """A contiguous (E, b, a) copy of the bf16 (E, a, b) tensor t, by the library's transpose kernel."""
+    E, A, B = t.shape
+    out = torch.empty((E, B, A), device=t.device, dtype=t.dtype)
+    call("mlora_transpose", ptr(t), E, A, B, t.stride(0), t.stride(1), t.stride(2), ptr(out), _lib.stream(t.device))
+    return out
 
 
 def _scale_args(scale, weight, backward: bool):
@@ -212,19 +220,26 @@ def _check_products(products_fp8):
                                   "fp8 stacks are decoded to bf16 in registers")
 
 
-def _reduce(g: torch.Tensor, low: torch.Tensor, offsets: torch.Tensor, scaling: float) -> torch.Tensor:
-    """(experts, N, R) bf16: scaling · sum over each expert's rows of g^T @ low (_grouped.py:362-370)."""
+def _reduce(g: torch.Tensor, low: torch.Tensor, offsets: torch.Tensor, scaling: float,
+            transposed: bool = False) -> torch.Tensor:
+    """(experts, N, R) bf16: scaling · sum over each expert's rows of g^T @ low (_grouped.py:362-370);
+    (experts, R, N), written in that layout by the kernel, when transposed."""
     experts = offsets.numel()
     rows, N = g.shape
     R = low.shape[1]
     if g.stride(1) != 1 or g.stride(0) % 8 or g.data_ptr() % 16:
         g = g.contiguous()
-    out = torch.empty((experts, N, R), device=g.device, dtype=torch.bfloat16)
+    if transposed:
+        out = torch.empty((experts, R, N), device=g.device, dtype=torch.bfloat16)
+        o_se, o_sn, o_sr = out.stride(0), out.stride(2), out.stride(1)
+    else:
+        out = torch.empty((experts, N, R), device=g.device, dtype=torch.bfloat16)
+        o_se, o_sn, o_sr = out.stride(0), out.stride(1), out.stride(2)
     info = {"rows": rows, "N": N, "R": R}
     if launch_observer is not None:
         launch_observer("grouped_reduce", "before", info)
     call("mlora_grouped_reduce", ptr(g), g.stride(0), ptr(low), low.stride(0), rows, N, R, float(scaling),
-         ptr(offsets), experts, ptr(out), out.stride(0), out.stride(1), out.stride(2), _lib.stream(g.device))
+         ptr(offsets), experts, ptr(out), o_se, o_sn, o_sr, _lib.stream(g.device))
     if launch_observer is not None:
         launch_observer("grouped_reduce", "after", info)
     return out
@@ -258,13 +273,15 @@ class _LoraGroupedProduct(torch.autograd.Function):
         # grad_x = grad @ W (the stack read the other way) + scaling · bf16(grad @ B^T) @ A^T
         grad_x, low2 = _launch(grad_out, weight, ctx.scale, offsets, not ctx.is_transposed, adapters.swapped(),
                                ctx.scaling, None, True, backward=True)
-        grad_a = _reduce(x, low2, offsets, ctx.scaling)        # (experts, in, R): A's gradient, addressed (k, r)
-        grad_b = _reduce(grad_out, low, offsets, ctx.scaling)  # (experts, out, R): B's gradient, addressed (n, r)
+        # A's gradient (k, r) and B's (n, r), each written by the kernel in the layout of the factor it
+        # belongs to, so no copy follows
         rank = adapters.rank
         if ctx.is_transposed:  # A = lhs (in, rank), B = rhs (rank, out)
-            grad_lhs, grad_rhs = grad_a[:, :, :rank], grad_b.transpose(1, 2)[:, :rank, :]
+            grad_lhs = _reduce(x, low2, offsets, ctx.scaling)[:, :, :rank]
+            grad_rhs = _reduce(grad_out, low, offsets, ctx.scaling, transposed=True)[:, :rank, :]
         else:  # A = rhs^T, B = lhs^T
-            grad_lhs, grad_rhs = grad_b[:, :, :rank], grad_a.transpose(1, 2)[:, :rank, :]
+            grad_rhs = _reduce(x, low2, offsets, ctx.scaling, transposed=True)[:, :rank, :]
+            grad_lhs = _reduce(grad_out, low, offsets, ctx.scaling)[:, :, :rank]
         if ctx.lhs_dtype is not None and ctx.lhs_dtype != torch.bfloat16:
             grad_lhs, grad_rhs = grad_lhs.to(ctx.lhs_dtype), grad_rhs.to(ctx.lhs_dtype)
         return grad_x, None, None, None, None, grad_lhs, grad_rhs, None, None, None

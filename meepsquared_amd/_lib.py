@@ -43,6 +43,7 @@ SIGNATURES = {
     "mlora_swiglu_backward": (c_int, [P, P, I64, I64, P, P]),
     "mlora_combine": (c_int, [P, I64, P, c_int, P, I64, c_int, P, c_int, P, P]),
     "mlora_combine_backward": (c_int, [P, P, I64, P, c_int, P, I64, c_int, P, c_int, P, P, P]),
+    "mlora_transpose": (c_int, [P, I64, I64, I64, I64, I64, I64, P, P]),
     "mlora_fp8_quantize": (c_int, [P, c_int, I64, I64, I64, c_int, c_int, P, P, P]),
     "mlora_fp8_dequantize": (c_int, [P, P, I64, I64, I64, c_int, c_int, P, c_int, P]),
     "mlora_nf4_workspace_bytes": (c_size_t, [I64]),
@@ -53,7 +54,7 @@ SIGNATURES = {
 
 def _load():
     if not LIBRARY.exists():
-        raise ImportError(f"{LIBRARY} is missing: build it with `python -m meepsquared_amd._build` "
+        raise ImportError(f"{LIBRARY} is missing: build it with `python meepsquared_amd/_build.py` "
                           "(or __graft_entry__.build()); the operator has no other implementation")
     lib = ctypes.CDLL(str(LIBRARY))
     for name, (res, args) in SIGNATURES.items():

@@ -268,3 +268,44 @@ extern "C" int mlora_combine_backward(const void* dout, const void* y, int64_t H
     return fail("combine_backward: weight dtype %d is not bf16/f32", w_dtype);
   return launch_status("combine_backward");
 }
+
+// ---- adapter layouts ----
+// dst[e][b][a] = src[e*s_e + a*s_a + b*s_b]: a batched transpose into a contiguous (E, B, A) bf16
+// tensor, through a 64 x 64 LDS tile (reads along b, writes along a).  Used for the adapters'
+// roles in the input-gradient product (src/meepsquared/_grouped.py:304-310 addresses the same
+// factors by strides; the kernel here takes them k-contiguous).
+namespace mlora {
+
+__global__ __launch_bounds__(256) void transpose_kernel(const bf16* __restrict__ src, int64_t A, int64_t B,
+                                                        int64_t s_e, int64_t s_a, int64_t s_b, bf16* __restrict__ dst) {
+  __shared__ bf16 tile[64][66];
+  const int64_t e = blockIdx.z, a0 = (int64_t)blockIdx.y * 64, b0 = (int64_t)blockIdx.x * 64;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;  // 64 x 4
+  const bf16* s = src + e * s_e;
+#pragma unroll 4
+  for (int i = ty; i < 64; i += 4) {
+    const int64_t a = a0 + i, b = b0 + tx;
+    if (a < A && b < B) tile[i][tx] = s[a * s_a + b * s_b];
+  }
+  __syncthreads();
+  bf16* d = dst + e * A * B;
+#pragma unroll 4
+  for (int j = ty; j < 64; j += 4) {
+    const int64_t b = b0 + j, a = a0 + tx;
+    if (a < A && b < B) d[b * A + a] = tile[tx][j];
+  }
+}
+
+}  // namespace mlora
+
+extern "C" int mlora_transpose(const void* src, int64_t E, int64_t A, int64_t B, int64_t s_e, int64_t s_a,
+                               int64_t s_b, void* dst, void* stream) {
+  clear_error();
+  if (E < 0 || A < 0 || B < 0) return fail("transpose: negative size");
+  if (E == 0 || A == 0 || B == 0) return 0;
+  if (E > 65535 || (A + 63) / 64 > 65535 || (B + 63) / 64 > 0x7FFFFFFF)
+    return fail("transpose: (E=%lld, A=%lld, B=%lld) exceeds the grid", (long long)E, (long long)A, (long long)B);
+  hipLaunchKernelGGL(transpose_kernel, dim3((unsigned)((B + 63) / 64), (unsigned)((A + 63) / 64), (unsigned)E),
+                     dim3(256), 0, as_stream(stream), (const bf16*)src, A, B, s_e, s_a, s_b, (bf16*)dst);
+  return launch_status("transpose");
+}

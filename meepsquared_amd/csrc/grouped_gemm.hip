@@ -591,7 +591,9 @@ extern "C" int mlora_grouped_gemm(const void* x, int64_t ldx, int64_t rows, int 
   if (ldx < K || ldx % 8 || !aligned(x, 16))
     return fail("grouped_gemm: x needs a 16-byte aligned base and a row stride (%lld) that is a multiple of 8 and >= K",
                 (long long)ldx);
-  if (ldo < N) return fail("grouped_gemm: ldo=%lld < N=%d", (long long)ldo, N);
+  if (ldo < N || ldo % 8 || !aligned(out, 16))
+    return fail("grouped_gemm: out needs a 16-byte aligned base and a row stride (%lld) that is a multiple of 8 and >= N",
+                (long long)ldo);
   if ((int64_t)BM * ldx * 2 > 0x7FFFFFF0) return fail("grouped_gemm: row stride %lld too large", (long long)ldx);
   const bool bkc = w_sk == 1;
   if (!bkc && w_sn != 1)

@@ -185,3 +185,25 @@ def test_qwen3_moe_sized_projection_stays_within_tolerance():
     got, expected = run_both(x, weight, None, offsets, False, lhs, rhs, 2.0, None)
     for name, a, b in zip(("out", "grad_x", "grad_lhs", "grad_rhs"), got, expected):
         assert rel(a, b) < BF16_TOL, (name, rel(a, b))
+
+
+@pytest.mark.parametrize("E,A,B", [(3, 16, 200), (2, 130, 48), (1, 64, 64), (5, 1, 7)])
+def test_the_batched_transpose_is_exact(E, A, B):
+    """mlora_transpose (the adapters' roles in the input-gradient product): exact, any strides."""
+    from meepsquared_amd._grouped import _transposed
+
+    torch.manual_seed(E * 1000 + A + B)
+    t = torch.randn(E, A, B, device="cuda").bfloat16()
+    assert torch.equal(_transposed(t), t.transpose(1, 2).contiguous())
+    s = torch.randn(E, B, A, device="cuda").bfloat16().transpose(1, 2)  # a strided view
+    assert torch.equal(_transposed(s), s.transpose(1, 2).contiguous())
+
+
+def test_the_swapped_adapters_take_each_others_roles():
+    from meepsquared_amd import _grouped
+
+    lhs, rhs = torch.randn(3, 10, 4, device="cuda"), torch.randn(3, 4, 12, device="cuda")
+    a = _grouped._Adapters(lhs, rhs, False)
+    sw = a.swapped()
+    assert sw.at.shape == (3, 16, 10) and sw.bt.shape == (3, 12, 16) and sw.rank == 4
+    assert torch.equal(sw.at, a.bt.transpose(1, 2)) and torch.equal(sw.bt, a.at.transpose(1, 2))
