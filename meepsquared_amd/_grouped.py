@@ -18,6 +18,8 @@ lora_linear (:408-417).  The per-expert float32 references (:420-444) are test o
 in the repository's `oracle/` package, not here.
 """
 
+import os
+
 import torch
 
 from meepsquared_amd import _lib
@@ -149,11 +151,15 @@ def _scale_args(scale, weight, backward: bool):
     raise ValueError(f"scale of shape {tuple(scale.shape)} is neither (experts,) nor (experts, out)")
 
 
-def _launch(x, weight, scale, offsets, is_transposed, adapters, scaling, bias, store_low, backward=False):
-    """One launch of the product kernel. Returns (out, low), low None without adapters or store_low."""
+def _launch(x, weight, scale, offsets, is_transposed, adapters, scaling, bias, store_low, backward=False,
+            products_fp8=False):
+    """One launch of the product kernel. Returns (out, low), low None without adapters or store_low.
+    products_fp8: the fp8 products (only for an fp8 stack; resolved by the caller as _x_fp8 does)."""
     _lib.require_gpu(x, offsets)
     if x.dtype != torch.bfloat16:
         raise TypeError(f"x is {x.dtype}; the kernel computes in bf16")
+    if products_fp8:
+        return _launch_fp8(x, weight, scale, offsets, is_transposed, adapters, scaling, bias, store_low, backward)
     rows, K = x.shape
     if x.stride(1) != 1 or x.stride(0) % 8 or x.data_ptr() % 16:
         x = x.contiguous()
@@ -210,14 +216,86 @@ def grouped_linear(x: torch.Tensor, weight, offsets: torch.Tensor, is_transposed
     scale in.  The base product alone (src/meepsquared/_grouped.py:348-359); block_m is accepted
     for the reference's signature, the kernel's own tiling is fixed.
     """
-    _check_products(products_fp8)
-    return _launch(x, weight, None, offsets, is_transposed, None, 1.0, None, False)[0]
+    return _launch(x, weight, None, offsets, is_transposed, None, 1.0, None, False,
+                   products_fp8=_x_fp8(weight, products_fp8))[0]
 
 
-def _check_products(products_fp8):
-    if products_fp8:
-        raise NotImplementedError("fp8 products (activations quantised to e4m3 on the MFMA) are not built; "
-                                  "fp8 stacks are decoded to bf16 in registers")
+def fp8_products(device=None) -> bool:
+    """Whether an fp8 stack's products run on the fp8 MFMA with the activations quantised to e4m3 when
+    the caller does not say: MEEPSQUARED_FP8_PRODUCTS=1, as src/meepsquared/_grouped.py:70-80."""
+    return os.environ.get("MEEPSQUARED_FP8_PRODUCTS") == "1"
+
+
+def _x_fp8(weight, products_fp8) -> bool:
+    """The reference's X_FP8 (src/meepsquared/_grouped.py:320): only an fp8 stack, and then the switch."""
+    w_fp8 = isinstance(weight, torch.Tensor) and weight.dtype == torch.float8_e4m3fn
+    return w_fp8 and (fp8_products() if products_fp8 is None else bool(products_fp8))
+
+
+def _k_contiguous(weight, w_se, w_sk, w_sn, K, N):
+    """The fp8 stack addressed W[e][n][k] with k contiguous: the stack itself, or a transposed copy
+    made by the library's byte transpose and kept on the stack tensor for as long as the tensor
+    lives and is not modified in place (the stacks are frozen: made once, reused every step)."""
+    if w_sk == 1:
+        return weight, w_se, w_sn
+    key = (tuple(weight.shape), tuple(weight.stride()), weight.data_ptr(), weight._version, K, N)
+    held = getattr(weight, "_mlora_k_contiguous", None)
+    if held is None or held[0] != key:
+        E = weight.shape[0]
+        t = torch.empty((E, N, K), device=weight.device, dtype=torch.uint8)
+        call("mlora_transpose_u8", ptr(weight), E, K, N, w_se, w_sk, w_sn, ptr(t), _lib.stream(weight.device))
+        held = (key, t)
+        weight._mlora_k_contiguous = held
+    t = held[1]
+    return t, t.stride(0), t.stride(1)
+
+
+def _launch_fp8(x, weight, scale, offsets, is_transposed, adapters, scaling, bias, store_low, backward):
+    """The fp8 products: one fp8_prep pass over x (e4m3 values, power-of-two scales per row and 64
+    columns, and low = bf16(x · A_e)), then the fp8 grouped product on the block-scaled MFMA."""
+    rows, K = x.shape
+    if K % 16:
+        raise ValueError(f"the fp8 products need in={K} to be a multiple of 16")
+    if x.stride(1) != 1 or x.stride(0) % 8 or x.data_ptr() % 16:
+        x = x.contiguous()
+    N, w_se, w_sk, w_sn = _stack_strides(weight, K, is_transposed)
+    out = torch.empty((rows, N), device=x.device, dtype=x.dtype)
+    R = adapters.padded if adapters is not None else 0
+    low = torch.empty((rows, R), device=x.device, dtype=torch.bfloat16) if adapters is not None else None
+    if rows == 0:
+        return out, (low if store_low else None)
+    offsets = offsets if offsets.dtype == torch.int32 else offsets.to(torch.int32)
+    offsets = offsets.contiguous()
+    _lib.require_gpu(weight)
+    scale, scale_kind, scale_se, scale_on_k = _scale_args(scale, weight, backward)
+    colscale, cs_se = None, 0
+    if scale_kind == _lib.SCALE_ROW and scale_on_k:  # a per-row stack scale along k: folded into x
+        colscale, cs_se, scale, scale_kind, scale_se = scale, scale_se, None, _lib.SCALE_NONE, 0
+    w8, w_se, w_sn = _k_contiguous(weight, w_se, w_sk, w_sn, K, N)
+    nkb = (K + 63) // 64
+    x8 = torch.empty((rows, nkb * 64), device=x.device, dtype=torch.uint8)
+    xs = torch.empty((nkb, rows), device=x.device, dtype=torch.int32)
+    E = offsets.numel()
+    if bias is not None:
+        bias = bias.to(torch.bfloat16)
+        if bias.stride(-1) != 1:
+            bias = bias.contiguous()
+    at = adapters.at if adapters is not None else None
+    bt = adapters.bt if adapters is not None else None
+    info = {"rows": rows, "K": K, "N": N, "rank": adapters.rank if adapters is not None else 0, "fp8": True}
+    if launch_observer is not None:
+        launch_observer("grouped_gemm", "before", info)
+    stream = _lib.stream(x.device)
+    call("mlora_fp8_prep", ptr(x), x.stride(0), rows, K, ptr(colscale), cs_se, ptr(x8), x8.stride(0), ptr(xs),
+         xs.stride(0), ptr(at), at.stride(0) if at is not None else 0, at.stride(1) if at is not None else 0, R,
+         ptr(low), low.stride(0) if low is not None else 0, ptr(offsets), E, stream)
+    call("mlora_fp8_gemm", ptr(x8), x8.stride(0), ptr(xs), xs.stride(0), rows, K, N, ptr(w8), w_se, w_sn,
+         ptr(scale), scale_kind, scale_se, ptr(low), low.stride(0) if low is not None else 0,
+         ptr(bt), bt.stride(0) if bt is not None else 0, bt.stride(1) if bt is not None else 0, R, float(scaling),
+         ptr(bias), bias.stride(0) if bias is not None else 0, ptr(out), out.stride(0), ptr(offsets), E, stream)
+    if launch_observer is not None:
+        launch_observer("grouped_gemm", "after", info)
+    return out, (low if store_low else None)
 
 
 def _reduce(g: torch.Tensor, low: torch.Tensor, offsets: torch.Tensor, scaling: float,
@@ -250,10 +328,11 @@ class _LoraGroupedProduct(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, x, weight, scale, offsets, is_transposed, lhs, rhs, scaling, bias, products_fp8):
-        _check_products(products_fp8)
+        x_fp8 = _x_fp8(weight, products_fp8)
         offsets = offsets.to(torch.int32).contiguous()
         adapters = _Adapters(lhs, rhs, is_transposed) if lhs is not None else None
-        out, low = _launch(x, weight, scale, offsets, is_transposed, adapters, scaling, bias, True)
+        out, low = _launch(x, weight, scale, offsets, is_transposed, adapters, scaling, bias, True, products_fp8=x_fp8)
+        ctx.x_fp8 = x_fp8
         ctx.save_for_backward(x, offsets, *((low,) if low is not None else ()))
         ctx.weight = weight  # frozen: held as it is (an NF4 stack is not a tensor)
         ctx.adapters, ctx.scale, ctx.is_transposed, ctx.scaling = adapters, scale, is_transposed, scaling
@@ -267,12 +346,12 @@ class _LoraGroupedProduct(torch.autograd.Function):
         grad_out = grad_out.to(torch.bfloat16).contiguous()
         if adapters is None:
             grad_x, _ = _launch(grad_out, weight, ctx.scale, offsets, not ctx.is_transposed, None, 1.0, None, False,
-                                backward=True)
+                                backward=True, products_fp8=ctx.x_fp8)
             return grad_x, None, None, None, None, None, None, None, None, None
         low = rest[0]
         # grad_x = grad @ W (the stack read the other way) + scaling · bf16(grad @ B^T) @ A^T
         grad_x, low2 = _launch(grad_out, weight, ctx.scale, offsets, not ctx.is_transposed, adapters.swapped(),
-                               ctx.scaling, None, True, backward=True)
+                               ctx.scaling, None, True, backward=True, products_fp8=ctx.x_fp8)
         # A's gradient (k, r) and B's (n, r), each written by the kernel in the layout of the factor it
         # belongs to, so no copy follows
         rank = adapters.rank

@@ -49,6 +49,26 @@ __device__ __forceinline__ float fp8_e4m3_to_f32(uint32_t byte) {
   return e ? normal : sub;
 }
 
+// fp32 -> OCP e4m3fn with round-to-nearest-even.  Magnitudes from 464 up (and NaN) give NaN
+// (0x7F | sign), as torch's float8_e4m3fn conversion does; 448 < |v| < 464 round to 448.
+__device__ __forceinline__ uint32_t f32_to_e4m3(float v) {
+  uint32_t b = __float_as_uint(v);
+  const uint32_t sign = (b >> 24) & 0x80u;
+  b &= 0x7FFFFFFFu;
+  if (b >= 0x43E80000u) return sign | 0x7Fu;  // >= 464 or NaN
+  if (b < 0x3C800000u) {                       // below 2^-6: subnormal range, units of 2^-9
+    // add 2^-9 * 2^23 style bias: rounding of the integer count of 2^-9 steps, ties to even
+    const float steps = __uint_as_float(b) * 512.0f;  // exact (power-of-two scaling)
+    const float r = __builtin_rintf(steps);           // nearest, ties to even
+    return sign | (uint32_t)r;                        // r <= 8 -> 8 is the smallest normal 0x08
+  }
+  // normal: keep 3 mantissa bits, round to nearest even on the dropped 20 bits
+  const uint32_t lsb = (b >> 20) & 1u;
+  b += 0x7FFFFu + lsb;
+  const uint32_t exp = (b >> 23) - 120u;  // rebias 127 -> 7
+  return sign | (exp << 3) | ((b >> 20) & 7u);
+}
+
 // ---- wave primitives (wave64) ----
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

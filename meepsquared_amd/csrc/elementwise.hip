@@ -276,19 +276,20 @@ extern "C" int mlora_combine_backward(const void* dout, const void* y, int64_t H
 // factors by strides; the kernel here takes them k-contiguous).
 namespace mlora {
 
-__global__ __launch_bounds__(256) void transpose_kernel(const bf16* __restrict__ src, int64_t A, int64_t B,
-                                                        int64_t s_e, int64_t s_a, int64_t s_b, bf16* __restrict__ dst) {
-  __shared__ bf16 tile[64][66];
+template <typename T>
+__global__ __launch_bounds__(256) void transpose_kernel(const T* __restrict__ src, int64_t A, int64_t B,
+                                                        int64_t s_e, int64_t s_a, int64_t s_b, T* __restrict__ dst) {
+  __shared__ T tile[64][66];
   const int64_t e = blockIdx.z, a0 = (int64_t)blockIdx.y * 64, b0 = (int64_t)blockIdx.x * 64;
   const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;  // 64 x 4
-  const bf16* s = src + e * s_e;
+  const T* s = src + e * s_e;
 #pragma unroll 4
   for (int i = ty; i < 64; i += 4) {
     const int64_t a = a0 + i, b = b0 + tx;
     if (a < A && b < B) tile[i][tx] = s[a * s_a + b * s_b];
   }
   __syncthreads();
-  bf16* d = dst + e * A * B;
+  T* d = dst + e * A * B;
 #pragma unroll 4
   for (int j = ty; j < 64; j += 4) {
     const int64_t b = b0 + j, a = a0 + tx;
@@ -305,7 +306,19 @@ extern "C" int mlora_transpose(const void* src, int64_t E, int64_t A, int64_t B,
   if (E == 0 || A == 0 || B == 0) return 0;
   if (E > 65535 || (A + 63) / 64 > 65535 || (B + 63) / 64 > 0x7FFFFFFF)
     return fail("transpose: (E=%lld, A=%lld, B=%lld) exceeds the grid", (long long)E, (long long)A, (long long)B);
-  hipLaunchKernelGGL(transpose_kernel, dim3((unsigned)((B + 63) / 64), (unsigned)((A + 63) / 64), (unsigned)E),
+  hipLaunchKernelGGL(transpose_kernel<bf16>, dim3((unsigned)((B + 63) / 64), (unsigned)((A + 63) / 64), (unsigned)E),
                      dim3(256), 0, as_stream(stream), (const bf16*)src, A, B, s_e, s_a, s_b, (bf16*)dst);
   return launch_status("transpose");
+}
+
+extern "C" int mlora_transpose_u8(const void* src, int64_t E, int64_t A, int64_t B, int64_t s_e, int64_t s_a,
+                                  int64_t s_b, void* dst, void* stream) {
+  clear_error();
+  if (E < 0 || A < 0 || B < 0) return fail("transpose_u8: negative size");
+  if (E == 0 || A == 0 || B == 0) return 0;
+  if (E > 65535 || (A + 63) / 64 > 65535 || (B + 63) / 64 > 0x7FFFFFFF)
+    return fail("transpose_u8: (E=%lld, A=%lld, B=%lld) exceeds the grid", (long long)E, (long long)A, (long long)B);
+  hipLaunchKernelGGL(transpose_kernel<uint8_t>, dim3((unsigned)((B + 63) / 64), (unsigned)((A + 63) / 64), (unsigned)E),
+                     dim3(256), 0, as_stream(stream), (const uint8_t*)src, A, B, s_e, s_a, s_b, (uint8_t*)dst);
+  return launch_status("transpose_u8");
 }

@@ -36,6 +36,47 @@ def fp8_dequantize(q, scale, is_transposed=False):
     return q * (scale.unsqueeze(1) if is_transposed else scale.unsqueeze(2))
 
 
+def fp8_rows_quantize(x, block=64, colscale=None):
+    """Activations for the fp8 products: per row and per `block` columns, the power of two 2^e with
+    amax·2^-e <= 448 (e the smallest such integer; e = 0 for an all-zero block) and the values
+    e4m3(x·2^-e) rounded to nearest even.  Returns (q uint8 (rows, K padded to block), e8m0 int32
+    (blocks, rows) = 127 + e).  colscale (K,) multiplies the columns first.
+
+    The reference quantises per row and per BLOCK_K tile with scale amax/448
+    (src/meepsquared/_grouped.py:191-194); this is that rule with the scale rounded up to a power of
+    two, the form the block-scaled fp8 MFMA applies.
+    Pinned by: torch's float8_e4m3fn cast (a library) for the values and, for the exponent, the
+    brute-force definition min{e : amax·2^-e <= 448} (tests/test_oracle.py).
+    """
+    x = torch.as_tensor(x).float()
+    if colscale is not None:
+        x = x * torch.as_tensor(colscale).float()
+    rows, K = x.shape
+    kp = -(-K // block) * block
+    xp = torch.zeros(rows, kp)
+    xp[:, :K] = x
+    xb = xp.view(rows, kp // block, block)
+    amax = xb.abs().amax(dim=2)
+    e = torch.zeros_like(amax, dtype=torch.int64)
+    nz = amax > 0
+    # smallest integer e with amax * 2^-e <= 448: ceil(log2(amax / 448)), exact in float64
+    e[nz] = torch.ceil(torch.log2(amax[nz].double() / E4M3_MAX)).to(torch.int64)
+    # guard the float64 log2 at exact powers of two
+    over = nz & (amax.double() * torch.pow(2.0, -e.double()) > E4M3_MAX)
+    e[over] += 1
+    q = (xb * torch.pow(2.0, -e.float()).unsqueeze(2)).to(torch.float8_e4m3fn).view(rows, kp)
+    return q.view(torch.uint8), (127 + e).to(torch.int32).t().contiguous()
+
+
+def fp8_rows_dequantize(q, e8m0, K):
+    """q · 2^(e8m0 - 127) per row and block, the first K columns (float32)."""
+    rows, kp = q.shape
+    block = kp // e8m0.shape[0]
+    v = q.view(torch.float8_e4m3fn).float().view(rows, kp // block, block)
+    v = v * torch.pow(2.0, (e8m0.t().float() - 127)).unsqueeze(2)
+    return v.view(rows, kp)[:, :K]
+
+
 def nf4_code_from_definition():
     """The 16 NF4 values from QLoRA's definition (Dettmers et al. 2023, Appendix E): 8 positive
     quantiles of N(0,1) from the upper half (offset 0.9677 = 1/2 (1/(2·15) + 1/(2·16)) mapped to

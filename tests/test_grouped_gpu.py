@@ -6,6 +6,7 @@ import pytest
 import torch
 
 from helpers import offsets_of, rel
+from oracle import formats
 from oracle import grouped as ref
 
 pytestmark = pytest.mark.gpu
@@ -71,10 +72,11 @@ def adapters(experts, K, N, rank, is_transposed):
     return lhs.requires_grad_(), rhs.requires_grad_()
 
 
-def run_both(x, weight, scale, offsets, is_transposed, lhs, rhs, scaling, bias, ref_weight=None, ref_scale="same"):
+def run_both(x, weight, scale, offsets, is_transposed, lhs, rhs, scaling, bias, ref_weight=None, ref_scale="same",
+             products_fp8=None):
     from meepsquared_amd import lora_linear
 
-    out = lora_linear(x, weight, scale, offsets, is_transposed, lhs, rhs, scaling, bias)
+    out = lora_linear(x, weight, scale, offsets, is_transposed, lhs, rhs, scaling, bias, products_fp8)
     grad = torch.randn_like(out)
     out.backward(grad)
     got = (out.detach(), x.grad.clone(), lhs.grad.clone(), rhs.grad.clone())
@@ -89,7 +91,7 @@ def run_both(x, weight, scale, offsets, is_transposed, lhs, rhs, scaling, bias, 
 
 
 @pytest.mark.parametrize("is_transposed", [False, True])
-@pytest.mark.parametrize("fp8", [False, "expert", "row"])
+@pytest.mark.parametrize("fp8", [False, "expert", "row", "products", "products_row"])
 @pytest.mark.parametrize("rank", [4, 16, 40])
 def test_the_product_with_adapters_and_its_gradients_match_pytorch(is_transposed, fp8, rank):
     from meepsquared_amd import _fp8
@@ -104,14 +106,20 @@ def test_the_product_with_adapters_and_its_gradients_match_pytorch(is_transposed
     weight = torch.randn(shape, device="cuda", dtype=torch.bfloat16) * 0.05
     scale = None
     if fp8:
-        weight, scale = _fp8.quantize_stack(weight, per_row=fp8 == "row", is_transposed=is_transposed)
+        weight, scale = _fp8.quantize_stack(weight, per_row=fp8.endswith("row"), is_transposed=is_transposed)
     lhs, rhs = adapters(experts, K, N, rank, is_transposed)
     bias = torch.randn(experts, N, device="cuda", dtype=torch.bfloat16)
+    products = bool(fp8) and fp8.startswith("products")
     got, expected = run_both(x, weight, scale, offsets, is_transposed, lhs, rhs, 2.0, bias,
-                             ref_weight=weight.float() if fp8 else None)
+                             ref_weight=weight.float() if fp8 else None, products_fp8=products)
     tol = Q_TOL if fp8 else BF16_TOL
     for name, a, b in zip(("out", "grad_x", "grad_lhs", "grad_rhs"), got, expected):
         assert a.shape == b.shape, name
+        if products and name in ("out", "grad_x"):
+            # activations (and the output gradient) quantised to e4m3 per row and 64 columns: the
+            # reference's own bound for its fp8 products (tests/test_grouped.py:136-139)
+            assert rel(a, b) <= 0.06, (name, rel(a, b))
+            continue
         assert rel(a, b) < tol, (name, rel(a, b))
         # the reference's own bound (tests/test_grouped.py:141-143)
         torch.testing.assert_close(a.float(), b.float(), atol=1e-2 * b.float().abs().max().item(), rtol=0, msg=name)
@@ -207,3 +215,61 @@ def test_the_swapped_adapters_take_each_others_roles():
     sw = a.swapped()
     assert sw.at.shape == (3, 16, 10) and sw.bt.shape == (3, 12, 16) and sw.rank == 4
     assert torch.equal(sw.at, a.bt.transpose(1, 2)) and torch.equal(sw.bt, a.at.transpose(1, 2))
+
+
+@pytest.mark.parametrize("is_transposed", [False, True])
+def test_the_fp8_product_quantizes_the_activations_per_row_and_stays_close(is_transposed):
+    """Mirrors the reference's tests/test_grouped.py:68-81 (products_fp8=True)."""
+    from meepsquared_amd import grouped_linear
+
+    torch.manual_seed(0)
+    x = torch.randn(300, 128, device="cuda", dtype=torch.bfloat16)
+    x[::7] *= 20  # rows of different sizes: the scale is per row
+    shape = (4, 128, 96) if is_transposed else (4, 96, 128)
+    weight = (torch.randn(shape, device="cuda") * 0.05).to(torch.float8_e4m3fn)
+    offsets = offsets_of([100, 0, 150, 50])
+    expected = ref.reference(x, weight.float(), offsets.cpu(), is_transposed).float().cpu()
+    out = grouped_linear(x, weight, offsets, is_transposed, products_fp8=True).float().cpu()
+    assert (out - expected).abs().max() <= 0.1 * expected.abs().max()
+    assert (out - expected).norm() / expected.norm() < 0.06
+
+
+def test_the_fp8_products_switch_follows_the_environment(monkeypatch):
+    from meepsquared_amd import _grouped
+
+    w8 = torch.zeros(2, 16, 32, device="cuda").to(torch.float8_e4m3fn)
+    wb = torch.zeros(2, 16, 32, device="cuda", dtype=torch.bfloat16)
+    monkeypatch.delenv("MEEPSQUARED_FP8_PRODUCTS", raising=False)
+    assert not _grouped._x_fp8(w8, None) and _grouped._x_fp8(w8, True) and not _grouped._x_fp8(wb, True)
+    monkeypatch.setenv("MEEPSQUARED_FP8_PRODUCTS", "1")
+    assert _grouped._x_fp8(w8, None) and not _grouped._x_fp8(w8, False)
+
+
+@pytest.mark.parametrize("K,colscale", [(208, False), (2048, False), (96, True)])
+def test_the_fp8_activation_pass_is_bit_exact(K, colscale):
+    """mlora_fp8_prep against the oracle: e4m3 bytes and E8M0 scales bit-exact; low = bf16(x · A_e)."""
+    from meepsquared_amd import _lib
+
+    torch.manual_seed(K)
+    counts = [37, 0, 130, 64, 1]
+    rows, E, R = sum(counts), len(counts), 16
+    offsets = offsets_of(counts)
+    x = (torch.randn(rows, K) * torch.logspace(-2, 2, rows).unsqueeze(1)).bfloat16().cuda()
+    at = (torch.randn(E, R, K) * 0.1).bfloat16().cuda()
+    cs = (torch.rand(E, K) + 0.5).cuda() if colscale else None
+    nkb = (K + 63) // 64
+    x8 = torch.empty(rows, nkb * 64, dtype=torch.uint8, device="cuda")
+    xs = torch.empty(nkb, rows, dtype=torch.int32, device="cuda")
+    low = torch.empty(rows, R, dtype=torch.bfloat16, device="cuda")
+    _lib.call("mlora_fp8_prep", _lib.ptr(x), x.stride(0), rows, K, _lib.ptr(cs), cs.stride(0) if cs is not None else 0,
+              _lib.ptr(x8), x8.stride(0), _lib.ptr(xs), xs.stride(0), _lib.ptr(at), at.stride(0), at.stride(1), R,
+              _lib.ptr(low), low.stride(0), _lib.ptr(offsets), E, _lib.stream())
+    torch.cuda.synchronize()
+    expert = torch.repeat_interleave(torch.arange(E), torch.tensor(counts))
+    xc = x.float().cpu()
+    scaled = xc * cs.cpu()[expert] if colscale else xc
+    q, e8 = formats.fp8_rows_quantize(scaled)
+    assert torch.equal(x8.cpu(), q)
+    assert torch.equal(xs.cpu(), e8)
+    low_ref = torch.einsum("rk,rjk->rj", xc.double(), at.cpu().double()[expert]).float()
+    assert rel(low.float().cpu(), low_ref) < 1e-2

@@ -239,3 +239,29 @@ def test_nf4_packs_the_first_value_in_the_high_nibble():
     packed, *_ = formats.nf4_quantize(x, NF4_CODE, dynamic_code())
     assert packed[0] == (15 << 4) | 0
     assert packed[1] == (7 << 4) | 7  # zeros
+
+
+def test_fp8_row_quantisation_picks_the_smallest_power_of_two_scale():
+    torch.manual_seed(3)
+    x = torch.randn(40, 200) * torch.logspace(-3, 3, 40).unsqueeze(1)
+    x[5] = 0.0
+    x[7, :64] = 448.0  # exactly at the limit: e = 0
+    x[8, :64] = 449.0  # just above: e = 1
+    q, e8 = formats.fp8_rows_quantize(x)
+    assert q.shape == (40, 256) and e8.shape == (4, 40)
+    xp = torch.zeros(40, 256)
+    xp[:, :200] = x
+    for r in range(40):
+        for b in range(4):
+            amax = xp[r, 64 * b:64 * b + 64].abs().max().item()
+            e = int(e8[b, r]) - 127
+            if amax == 0:
+                assert e == 0
+            else:  # brute force: the smallest e with amax * 2^-e <= 448
+                assert amax * 2.0 ** -e <= 448.0 and amax * 2.0 ** -(e - 1) > 448.0, (r, b, amax, e)
+    assert int(e8[0, 7]) == 127 and int(e8[0, 8]) == 128
+    back = formats.fp8_rows_dequantize(q, e8, 200)
+    # e4m3 keeps 3 mantissa bits: every normal value within 2^-4 relative
+    normal = back.abs() >= 2.0 ** -6 * torch.pow(2.0, e8.t().float() - 127).repeat_interleave(64, 1)[:, :200]
+    assert ((back - x).abs() <= x.abs() * 2.0 ** -4 + 1e-30)[normal].all()
+    assert not q[:, 200:].any()
