@@ -2,6 +2,7 @@
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline]
     python bench.py --copy-calibration MIB    # a plain device copy of known size, for PMC scaling
+    python bench.py --config 3                # config 3: fp8 e4m3 stacks with per-row scales, fp8 MFMA
 
 A step is one forward and backward pass of the routed MoE-LoRA layer over one batch of synthetic
 inputs already resident in HBM: router top-k softmax (from given logits), counting sort, gather,
@@ -29,6 +30,7 @@ sys.path.insert(0, str(ROOT))
 
 T, H, I, E, K_TOP, R, ALPHA = 8192, 2048, 768, 128, 8, 16, 32
 PEAK_BF16_TFLOPS = 2500.0
+PEAK_FP8_TFLOPS = 5000.0
 PROFILE_TRAFFIC = ROOT / "profiles" / "grouped_gemm_qwen3_traffic.txt"
 
 
@@ -142,6 +144,9 @@ def main():
     ap.add_argument("--cpu-tokens", type=int, default=T)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB")
+    ap.add_argument("--config", type=int, default=1, choices=(1, 3),
+                    help="1: the bf16 layer (default); 3: its stacks in fp8 e4m3 with one scale per output row, "
+                         "the products on the fp8 MFMA (activations quantised per row and 64 columns)")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {a.gpus})", file=sys.stderr)
@@ -158,7 +163,16 @@ def main():
     device = "cuda:0"
     torch.cuda.set_device(0)
     hidden, logits, gate_up, down, factors, dy = make_inputs(device)
-    experts = Experts(gate_up, down)
+    if a.config == 3:
+        from meepsquared_amd import _fp8
+
+        gate_up8, gate_up_s = _fp8.quantize_stack(gate_up, per_row=True)
+        down8, down_s = _fp8.quantize_stack(down, per_row=True)
+        del gate_up, down
+        experts = Experts(gate_up8, down8, gate_up_proj_scale_inv=gate_up_s, down_proj_scale_inv=down_s)
+        os.environ["MEEPSQUARED_FP8_PRODUCTS"] = "1"
+    else:
+        experts = Experts(gate_up, down)
     params = [hidden] + [t for (a_, b_, _) in factors.values() for t in (a_, b_)]
 
     def step():
@@ -220,23 +234,27 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
+        "dtype": "bf16" if a.config == 1 else "fp8-e4m3 products (bf16 activations, per-row fp32 stack scales)",
         "data": "synthetic (seeded N(0,1) x and logits, N(0,0.02) W, Kaiming-uniform A, N(0,0.01) B)",
-        "config": {"workload": "BASELINE config 1: Qwen3-30B-A3B-shaped MoE-LoRA layer fwd+bwd",
+        "config": {"workload": "BASELINE config 1: Qwen3-30B-A3B-shaped MoE-LoRA layer fwd+bwd" if a.config == 1 else
+                   "BASELINE config 3: config 1 with fp8-e4m3 stacks (per-row scales) on the fp8 MFMA",
                    "tokens": T, "hidden": H, "moe_intermediate": I, "experts": E, "top_k": K_TOP,
                    "lora_rank": R, "lora_alpha": ALPHA, "parallelism": "single GPU"},
         "step_tflops": round(flops / (ms_per_step / 1e3) / 1e12, 2),
         "step_frac_of_bf16_peak": round(flops / (ms_per_step / 1e3) / 1e12 / PEAK_BF16_TFLOPS, 4),
         "roofline": {"bound": "mfma", "kernel": "grouped_gemm_bf16_kernel (4 launches per step; traffic = mean HBM bytes per launch, rocprofv3 PMC)",
                      "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": read_traffic()},
+                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": read_traffic()} if a.config == 1 else
+                    {"bound": "mfma", "kernel": "fp8_prep + fp8_gemm_kernel (4 products per step, timed together)",
+                     "achieved": round(achieved, 2), "peak": PEAK_FP8_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK_FP8_TFLOPS, 4), "traffic": None},
         "kernel_ms_per_step": {"grouped_gemm": round(gemm_ms / a.steps, 4),
                                "grouped_reduce": round(sum(ms for _, ms in red) / a.steps, 4),
                                "rest": round(ms_per_step - (gemm_ms + sum(ms for _, ms in red)) / a.steps, 4)},
         "grouped_gemm_ms_by_shape": {k_: round(sum(v) / len(v), 4) for k_, v in per_shape.items()},
         "wall_s_timed": round(wall, 3),
     }
-    if not a.no_cpu_baseline:
+    if not a.no_cpu_baseline and a.config == 1:
         record["cpu_baseline"] = cpu_baseline(a.cpu_tokens)
     else:
         record["cpu_baseline"] = None

@@ -129,13 +129,24 @@ __global__ __launch_bounds__(PT) void fp8_prep_kernel(PrepArgs p) {
 #pragma unroll
   for (int rb = 0; rb < (NRB > 0 ? NRB : 1); ++rb) lacc[rb] = f32x4{};
   const int nkb = (p.K + PR - 1) / PR;
+  // this thread's two 8-column pieces of the 64 x 64 chunk, the next chunk's loaded while the
+  // current one is quantised (and A_e^T's chunk with them)
+  auto load_x = [&](int kb, int h) -> u32x4 {
+    const int c = tid + h * PT, row = c >> 3, cc = c & 7, col = kb * PR + cc * 8;
+    return (kb < nkb && row < mrows && col < p.K) ? *(const u32x4*)(p.x + (row0 + row) * p.ldx + col)
+                                                  : u32x4{0u, 0u, 0u, 0u};
+  };
+  u32x4 nx0 = load_x(0, 0), nx1 = load_x(0, 1);
   for (int kb = 0; kb < nkb; ++kb) {
+    const u32x4 cur[2] = {nx0, nx1};
+    nx0 = load_x(kb + 1, 0);
+    nx1 = load_x(kb + 1, 1);
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int c = tid + h * PT, row = c >> 3, cc = c & 7;
       const int col = kb * PR + cc * 8;
       const bool ok = row < mrows && col < p.K;
-      u32x4 v = ok ? *(const u32x4*)(p.x + (row0 + row) * p.ldx + col) : u32x4{0u, 0u, 0u, 0u};
+      const u32x4 v = cur[h];
       float f[8];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
