@@ -41,7 +41,15 @@ namespace dma {
 #define MLORA_DMA_OCC 1
 #endif
 
-constexpr int BM = 256, BN = 256, BK = 32, STAGES = 4;
+#ifndef MLORA_DMA_BK
+#define MLORA_DMA_BK 64
+#endif
+#ifndef MLORA_DMA_STAGES
+#define MLORA_DMA_STAGES 2
+#endif
+constexpr int BM = 256, BN = 256, BK = MLORA_DMA_BK, STAGES = MLORA_DMA_STAGES;
+constexpr int CPR = BK / 8;  // 16-byte chunks per [row][k] tile row
+static_assert((BK == 32 && STAGES == 4) || (BK == 64 && STAGES == 2), "ring shapes");
 constexpr int WAVES_M = MLORA_DMA_WM, WAVES_N = MLORA_DMA_WN;
 constexpr int NW = WAVES_M * WAVES_N, kThreads = 64 * NW;
 constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;
@@ -54,8 +62,10 @@ static_assert(FM >= 1 && FN >= 1 && (2 * FM) % WAVES_N == 0, "tile shape");
 
 typedef __attribute__((address_space(3))) void lds_void;
 
-// [row][k] tiles (rows of BK = 32 bf16, 4 chunks): chunk c of row r in slot c ^ ((r >> 2) & 3)
-__device__ __forceinline__ int swz_rk(int row, int chunk) { return row * BK + ((chunk ^ ((row >> 2) & 3)) << 3); }
+// [row][k] tiles (rows of BK bf16, CPR chunks of 16 bytes): chunk c of row r in slot c ^ f(r), with f
+// spreading the 16 rows one MFMA operand read touches over 16 distinct 16-byte bank groups
+__device__ __forceinline__ int swz_f(int row) { return (row >> (CPR == 4 ? 2 : 1)) & (CPR - 1); }
+__device__ __forceinline__ int swz_rk(int row, int chunk) { return row * BK + ((chunk ^ swz_f(row)) << 3); }
 // [k][n] tiles (rows of BN bf16): chunk c of row k in slot c ^ ((k & 3) << 2)
 __device__ __forceinline__ int swz_kn(int k, int chunk) { return k * BN + ((chunk ^ ((k & 3) << 2)) << 3); }
 
@@ -163,7 +173,7 @@ struct Feed {
 #pragma unroll
     for (int q = 0; q < XI; ++q) {
       const int instr = wave * XI + q, ci = instr * 64 + lane;
-      const int row = ci >> 2, c = (ci & 3) ^ ((row >> 2) & 3);
+      const int row = ci / CPR, c = (ci % CPR) ^ swz_f(row);
       xo[q] = (uint32_t)((row * p.ldx + c * 8) * 2);
       xk[q] = c * 8;
       xd[q] = instr * 512;
@@ -172,7 +182,7 @@ struct Feed {
     for (int q = 0; q < WI; ++q) {
       const int instr = wave * WI + q, ci = instr * 64 + lane;
       if constexpr (BKC) {  // [n][k]
-        const int row = ci >> 2, c = (ci & 3) ^ ((row >> 2) & 3);
+        const int row = ci / CPR, c = (ci % CPR) ^ swz_f(row);
         const int n = n0 + row;
         wo[q] = n < p.N ? (uint32_t)(((int64_t)n * p.w_sn + c * 8) * 2) : 0u;
         wk[q] = n < p.N ? c * 8 : (1 << 30);
@@ -190,7 +200,7 @@ struct Feed {
       // instruction block, the others masked off (their LDS bytes belong to other waves)
       const int c0 = wave * CPW, blk = c0 >> 6;
       const int ci = blk * 64 + lane;
-      const int r = ci >> 2, c = (ci & 3) ^ ((r >> 2) & 3);
+      const int r = ci / CPR, c = (ci % CPR) ^ swz_f(r);
       ao = (uint32_t)((r * p.at_sr + c * 8) * 2);
       ak = c * 8;
       ad = (BM + BN) * BK + blk * 512;
@@ -259,18 +269,21 @@ __device__ __forceinline__ void compute(const bf16* slot, int lane, int wm, int 
     }
     if constexpr (NRB > 0) {
       const bf16* aa = slot + (BM + BN) * BK;
-      bf16x8 ar[NRB];
 #pragma unroll
-      for (int rb = 0; rb < NRB; ++rb) ar[rb] = *(const bf16x8*)(aa + swz_rk(rb * 16 + (lane & 15), lane >> 4));
+      for (int ls = 0; ls < BK / 32; ++ls) {
+        bf16x8 ar[NRB];
 #pragma unroll
-      for (int q = 0; q < kLS; ++q) {
-        const int sh = wn + WAVES_N * q;  // this wave's 16-row half: block sh / 2, half sh % 2
-        if ((sh >> 1) < AM) {
-          const int rbase = ((sh >> 1) * WAVES_M + wm) * 32 + (sh & 1) * 16;
-          const bf16x8 xf = *(const bf16x8*)(as + swz_rk(rbase + (lane & 15), lane >> 4));
+        for (int rb = 0; rb < NRB; ++rb) ar[rb] = *(const bf16x8*)(aa + swz_rk(rb * 16 + (lane & 15), ls * 4 + (lane >> 4)));
 #pragma unroll
-          for (int rb = 0; rb < NRB; ++rb)
-            lacc[q][rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf, ar[rb], lacc[q][rb], 0, 0, 0);
+        for (int q = 0; q < kLS; ++q) {
+          const int sh = wn + WAVES_N * q;  // this wave's 16-row half: block sh / 2, half sh % 2
+          if ((sh >> 1) < AM) {
+            const int rbase = ((sh >> 1) * WAVES_M + wm) * 32 + (sh & 1) * 16;
+            const bf16x8 xf = *(const bf16x8*)(as + swz_rk(rbase + (lane & 15), ls * 4 + (lane >> 4)));
+#pragma unroll
+            for (int rb = 0; rb < NRB; ++rb)
+              lacc[q][rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf, ar[rb], lacc[q][rb], 0, 0, 0);
+          }
         }
       }
     }
@@ -294,18 +307,25 @@ template <int AM, bool BKC, int NRB>
 __device__ __forceinline__ void kloop(const GemmArgs& p, const Feed<BKC, NRB>& f, bf16* const (&slots)[STAGES], int nk,
                                       int lane, int wm, int wn, f32x16 (&acc)[FM][FN],
                                       f32x4 (&lacc)[kLS][NRB > 0 ? NRB : 1]) {
-  static_assert(STAGES == 4, "the unrolled loop below is written for four slots");
   int kt = 0;
-  for (; kt + STAGES <= nk; kt += STAGES) {
-    stage<0, AM, BKC, NRB>(p, f, slots, kt, lane, wm, wn, acc, lacc);
-    stage<1, AM, BKC, NRB>(p, f, slots, kt + 1, lane, wm, wn, acc, lacc);
-    stage<2, AM, BKC, NRB>(p, f, slots, kt + 2, lane, wm, wn, acc, lacc);
-    stage<3, AM, BKC, NRB>(p, f, slots, kt + 3, lane, wm, wn, acc, lacc);
+  if constexpr (STAGES == 4) {
+    for (; kt + STAGES <= nk; kt += STAGES) {
+      stage<0, AM, BKC, NRB>(p, f, slots, kt, lane, wm, wn, acc, lacc);
+      stage<1, AM, BKC, NRB>(p, f, slots, kt + 1, lane, wm, wn, acc, lacc);
+      stage<2, AM, BKC, NRB>(p, f, slots, kt + 2, lane, wm, wn, acc, lacc);
+      stage<3, AM, BKC, NRB>(p, f, slots, kt + 3, lane, wm, wn, acc, lacc);
+    }
+    const int rem = nk - kt;  // 0 .. 3 stages left
+    if (rem > 0) stage<0, AM, BKC, NRB>(p, f, slots, kt, lane, wm, wn, acc, lacc);
+    if (rem > 1) stage<1, AM, BKC, NRB>(p, f, slots, kt + 1, lane, wm, wn, acc, lacc);
+    if (rem > 2) stage<2, AM, BKC, NRB>(p, f, slots, kt + 2, lane, wm, wn, acc, lacc);
+  } else {
+    for (; kt + 2 <= nk; kt += 2) {
+      stage<0, AM, BKC, NRB>(p, f, slots, kt, lane, wm, wn, acc, lacc);
+      stage<1, AM, BKC, NRB>(p, f, slots, kt + 1, lane, wm, wn, acc, lacc);
+    }
+    if (kt < nk) stage<0, AM, BKC, NRB>(p, f, slots, kt, lane, wm, wn, acc, lacc);
   }
-  const int rem = nk - kt;  // 0 .. 3 stages left
-  if (rem > 0) stage<0, AM, BKC, NRB>(p, f, slots, kt, lane, wm, wn, acc, lacc);
-  if (rem > 1) stage<1, AM, BKC, NRB>(p, f, slots, kt + 1, lane, wm, wn, acc, lacc);
-  if (rem > 2) stage<2, AM, BKC, NRB>(p, f, slots, kt + 2, lane, wm, wn, acc, lacc);
 }
 
 template <bool BKC, int NRB>
@@ -315,10 +335,14 @@ __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_ker
   constexpr int SE = SlotSize<NRB>::kElems;
   __shared__ __attribute__((aligned(16))) bf16 slot0[SE];
   __shared__ __attribute__((aligned(16))) bf16 slot1[SE];
+#if MLORA_DMA_STAGES == 4
   __shared__ __attribute__((aligned(16))) bf16 slot2[SE];
   __shared__ __attribute__((aligned(16))) bf16 slot3[SE];
-  extern __shared__ __attribute__((aligned(16))) int tile_map[];
   bf16* const slots[STAGES] = {slot0, slot1, slot2, slot3};
+#else
+  bf16* const slots[STAGES] = {slot0, slot1};
+#endif
+  extern __shared__ __attribute__((aligned(16))) int tile_map[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WAVES_N, wn = wave % WAVES_N;
@@ -470,7 +494,7 @@ __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_ker
 static size_t lds_bytes(int E) { return (size_t)E * sizeof(int); }
 static_assert(BM * (kMaxRank + 8) <= SlotSize<4>::kElems && BN * (kMaxRank + 8) <= SlotSize<4>::kElems,
               "the epilogue's low and B^T tiles must fit in the slots they reuse");
-static_assert(4 * SlotSize<4>::kElems * 2 + 4096 * 4 <= 163840, "four slots and the largest tile map fit in LDS");
+static_assert(STAGES * SlotSize<4>::kElems * 2 + 4096 * 4 <= 163840, "the slots and the largest tile map fit in LDS");
 
 template <bool BKC, int NRB>
 static int launch_t(const GemmArgs& a, hipStream_t s) {
