@@ -120,6 +120,18 @@ int mlora_grouped_gemm(const void* x, int64_t ldx, int64_t rows, int K, int N,
                        void* out, int64_t ldo, void* low, int64_t ldl,
                        const int32_t* offsets, int E, void* stream);
 
+/* mlora_grouped_gemm with the rows of x gathered: row r of the product is row gather[r] / k of x
+ * (x_rows rows, row stride ldx), so the expert-sorted copy h[perm // k] of the layer's input
+ * (src/meepsquared/_moe.py:80) is never written.  bf16 stacks only; the other arguments as
+ * mlora_grouped_gemm's (no per-row scale along k: the forward pass). */
+int mlora_grouped_gemm_gather(const void* x, int64_t ldx, int64_t x_rows, const int64_t* gather, int k, int64_t rows,
+                              int K, int N, const void* w, int w_dtype, int64_t w_se, int64_t w_sk, int64_t w_sn,
+                              const float* scale, int scale_kind, int64_t scale_se,
+                              const void* at, int64_t at_se, int64_t at_sr,
+                              const void* bt, int64_t bt_se, int64_t bt_sn, int rank, float scaling,
+                              const void* bias, int64_t bias_se, void* out, int64_t ldo, void* low, int64_t ldl,
+                              const int32_t* offsets, int E, void* stream);
+
 /* out[e, n, r] = bf16(scaling · sum over expert e's rows of g[row, n] · l[row, r]), fp32
  * accumulation in a fixed order, no atomics: the adapters' gradients.  g (rows, N) bf16 row stride
  * ldg; l (rows, R) bf16 row stride ldl; out addressed out[e*o_se + n*o_sn + r*o_sr].  R <= 64.
@@ -127,6 +139,12 @@ int mlora_grouped_gemm(const void* x, int64_t ldx, int64_t rows, int K, int N,
 int mlora_grouped_reduce(const void* g, int64_t ldg, const void* l, int64_t ldl, int64_t rows, int N, int R,
                          float scaling, const int32_t* offsets, int E,
                          void* out, int64_t o_se, int64_t o_sn, int64_t o_sr, void* stream);
+
+/* mlora_grouped_reduce with the rows of g gathered: row r is row gather[r] / k of g (A's gradient
+ * of the gate_up product when its input rows are gathered, as mlora_grouped_gemm_gather reads them). */
+int mlora_grouped_reduce_gather(const void* g, int64_t ldg, const int64_t* gather, int k, const void* l, int64_t ldl,
+                                int64_t rows, int N, int R, float scaling, const int32_t* offsets, int E,
+                                void* out, int64_t o_se, int64_t o_sn, int64_t o_sr, void* stream);
 
 /* ---------------------------------------------------------------------------------------------
  * The layer around the products: gather, SwiGLU, combine (bf16 activations)

@@ -299,11 +299,13 @@ def _launch_fp8(x, weight, scale, offsets, is_transposed, adapters, scaling, bia
 
 
 def _reduce(g: torch.Tensor, low: torch.Tensor, offsets: torch.Tensor, scaling: float,
-            transposed: bool = False) -> torch.Tensor:
+            transposed: bool = False, gather=None) -> torch.Tensor:
     """(experts, N, R) bf16: scaling · sum over each expert's rows of g^T @ low (_grouped.py:362-370);
-    (experts, R, N), written in that layout by the kernel, when transposed."""
+    (experts, R, N), written in that layout by the kernel, when transposed.  gather = (perm, k): the
+    rows are g[perm // k] (g then has its own row count)."""
     experts = offsets.numel()
-    rows, N = g.shape
+    N = g.shape[1]
+    rows = low.shape[0] if gather is not None else g.shape[0]
     R = low.shape[1]
     if g.stride(1) != 1 or g.stride(0) % 8 or g.data_ptr() % 16:
         g = g.contiguous()
@@ -316,8 +318,13 @@ def _reduce(g: torch.Tensor, low: torch.Tensor, offsets: torch.Tensor, scaling: 
     info = {"rows": rows, "N": N, "R": R}
     if launch_observer is not None:
         launch_observer("grouped_reduce", "before", info)
-    call("mlora_grouped_reduce", ptr(g), g.stride(0), ptr(low), low.stride(0), rows, N, R, float(scaling),
-         ptr(offsets), experts, ptr(out), o_se, o_sn, o_sr, _lib.stream(g.device))
+    if gather is None:
+        call("mlora_grouped_reduce", ptr(g), g.stride(0), ptr(low), low.stride(0), rows, N, R, float(scaling),
+             ptr(offsets), experts, ptr(out), o_se, o_sn, o_sr, _lib.stream(g.device))
+    else:
+        perm, k = gather
+        call("mlora_grouped_reduce_gather", ptr(g), g.stride(0), ptr(perm), k, ptr(low), low.stride(0), rows, N, R,
+             float(scaling), ptr(offsets), experts, ptr(out), o_se, o_sn, o_sr, _lib.stream(g.device))
     if launch_observer is not None:
         launch_observer("grouped_reduce", "after", info)
     return out
@@ -364,6 +371,90 @@ class _LoraGroupedProduct(torch.autograd.Function):
         if ctx.lhs_dtype is not None and ctx.lhs_dtype != torch.bfloat16:
             grad_lhs, grad_rhs = grad_lhs.to(ctx.lhs_dtype), grad_rhs.to(ctx.lhs_dtype)
         return grad_x, None, None, None, None, grad_lhs, grad_rhs, None, None, None
+
+
+def gathered_product_fits(weight, products_fp8=None) -> bool:
+    """Whether the product can read its rows gathered from the layer's input: a bf16 stack tensor."""
+    return isinstance(weight, torch.Tensor) and weight.dtype == torch.bfloat16 and not _x_fp8(weight, products_fp8)
+
+
+class _GatheredLoraProduct(torch.autograd.Function):
+    """lora_linear of x = hidden[perm // k] without materialising x: the product and A's gradient read
+    the rows of hidden through perm (the fusion of src/meepsquared/_moe.py:80 into the gate_up product).
+    Gradients for hidden (each token's k rows summed) and the adapters."""
+
+    @staticmethod
+    def forward(ctx, hidden, perm, inv, k, weight, scale, offsets, is_transposed, lhs, rhs, scaling, bias):
+        _lib.require_gpu(hidden, perm, offsets, weight)
+        hidden = hidden if hidden.stride(-1) == 1 and hidden.stride(0) % 8 == 0 and hidden.data_ptr() % 16 == 0 \
+            else hidden.contiguous()
+        T, K = hidden.shape
+        rows = perm.numel()
+        offsets = offsets.to(torch.int32).contiguous()
+        adapters = _Adapters(lhs, rhs, is_transposed) if lhs is not None else None
+        N, w_se, w_sk, w_sn = _stack_strides(weight, K, is_transposed)
+        out = torch.empty((rows, N), device=hidden.device, dtype=torch.bfloat16)
+        R = adapters.padded if adapters is not None else 0
+        low = torch.empty((rows, R), device=hidden.device, dtype=torch.bfloat16) if adapters is not None else None
+        if rows:
+            scale_, scale_kind, scale_se, _ = _scale_args(scale, weight, False)
+            if bias is not None:
+                bias = bias.to(torch.bfloat16)
+                bias = bias if bias.stride(-1) == 1 else bias.contiguous()
+            at, bt = (adapters.at, adapters.bt) if adapters is not None else (None, None)
+            info = {"rows": rows, "K": K, "N": N, "rank": adapters.rank if adapters is not None else 0}
+            if launch_observer is not None:
+                launch_observer("grouped_gemm", "before", info)
+            call("mlora_grouped_gemm_gather", ptr(hidden), hidden.stride(0), T, ptr(perm), k, rows, K, N,
+                 ptr(weight), _lib.DT_BF16, w_se, w_sk, w_sn, ptr(scale_), scale_kind, scale_se,
+                 ptr(at), at.stride(0) if at is not None else 0, at.stride(1) if at is not None else 0,
+                 ptr(bt), bt.stride(0) if bt is not None else 0, bt.stride(1) if bt is not None else 0,
+                 R, float(scaling), ptr(bias), bias.stride(0) if bias is not None else 0,
+                 ptr(out), out.stride(0), ptr(low), low.stride(0) if low is not None else 0,
+                 ptr(offsets), offsets.numel(), _lib.stream(hidden.device))
+            if launch_observer is not None:
+                launch_observer("grouped_gemm", "after", info)
+        ctx.save_for_backward(hidden, perm, inv, offsets, *((low,) if low is not None else ()))
+        ctx.weight, ctx.adapters, ctx.scale = weight, adapters, scale
+        ctx.is_transposed, ctx.scaling, ctx.k = is_transposed, scaling, k
+        ctx.lhs_dtype = lhs.dtype if lhs is not None else None
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        hidden, perm, inv, offsets, *rest = ctx.saved_tensors
+        adapters, weight, k = ctx.adapters, ctx.weight, ctx.k
+        grad_out = grad_out.to(torch.bfloat16).contiguous()
+        T, K = hidden.shape
+        grad_lhs = grad_rhs = None
+        if adapters is None:
+            grad_sel, _ = _launch(grad_out, weight, ctx.scale, offsets, not ctx.is_transposed, None, 1.0, None, False,
+                                  backward=True)
+        else:
+            low = rest[0]
+            grad_sel, low2 = _launch(grad_out, weight, ctx.scale, offsets, not ctx.is_transposed, adapters.swapped(),
+                                     ctx.scaling, None, True, backward=True)
+            rank = adapters.rank
+            gather = (perm, k)
+            if ctx.is_transposed:
+                grad_lhs = _reduce(hidden, low2, offsets, ctx.scaling, gather=gather)[:, :, :rank]
+                grad_rhs = _reduce(grad_out, low, offsets, ctx.scaling, transposed=True)[:, :rank, :]
+            else:
+                grad_rhs = _reduce(hidden, low2, offsets, ctx.scaling, transposed=True, gather=gather)[:, :rank, :]
+                grad_lhs = _reduce(grad_out, low, offsets, ctx.scaling)[:, :, :rank]
+            if ctx.lhs_dtype is not None and ctx.lhs_dtype != torch.bfloat16:
+                grad_lhs, grad_rhs = grad_lhs.to(ctx.lhs_dtype), grad_rhs.to(ctx.lhs_dtype)
+        dh = torch.empty((T, K), device=grad_out.device, dtype=torch.bfloat16)
+        call("mlora_gather_rows_backward", ptr(grad_sel), K, ptr(inv), T, k, ptr(offsets), offsets.numel(),
+             ptr(dh), _lib.stream(grad_out.device))
+        return dh, None, None, None, None, None, None, None, grad_lhs, grad_rhs, None, None
+
+
+def lora_linear_gathered(hidden, perm, inv, k, weight, scale, offsets, is_transposed, lhs=None, rhs=None,
+                         scaling: float = 1.0, bias=None):
+    """lora_linear(hidden[perm // k], ...) with the gathered rows never materialised (bf16 stacks)."""
+    return _GatheredLoraProduct.apply(hidden, perm, inv, k, weight, scale, offsets, is_transposed, lhs, rhs, scaling,
+                                      bias)
 
 
 def lora_linear(x, weight, scale, offsets, is_transposed: bool, lhs=None, rhs=None, scaling: float = 1.0, bias=None,

@@ -196,7 +196,6 @@ def routed_forward(experts, hidden_states, top_k_index, top_k_weights, factors):
     num_tokens = hidden_states.shape[0]
     k = top_k_index.shape[-1]
     perm, inv, offsets = sort_by_expert(top_k_index, experts.num_experts)
-    selected = _Gather.apply(hidden_states, perm, inv, offsets, k)
 
     def project(x, name, bias_name):
         weight = getattr(experts, name)
@@ -205,7 +204,16 @@ def routed_forward(experts, hidden_states, top_k_index, top_k_weights, factors):
         return _grouped.lora_linear(x, weight, _stack_scale(experts, name), offsets, experts.is_transposed,
                                     lhs, rhs, scaling, bias)
 
-    act = _SwiGLU.apply(project(selected, "gate_up_proj", "gate_up_proj_bias"))
+    if hidden_states.dtype == torch.bfloat16 and _grouped.gathered_product_fits(experts.gate_up_proj):
+        # the gate_up product reads its rows straight from hidden_states through perm
+        lhs, rhs, scaling = factors.get("gate_up_proj", (None, None, 1.0))
+        bias = experts.gate_up_proj_bias if getattr(experts, "has_bias", False) else None
+        gate_up = _grouped.lora_linear_gathered(hidden_states, perm, inv, k, experts.gate_up_proj,
+                                                _stack_scale(experts, "gate_up_proj"), offsets, experts.is_transposed,
+                                                lhs, rhs, scaling, bias)
+    else:
+        gate_up = project(_Gather.apply(hidden_states, perm, inv, offsets, k), "gate_up_proj", "gate_up_proj_bias")
+    act = _SwiGLU.apply(gate_up)
     out = project(act, "down_proj", "down_proj_bias")
     result = _Combine.apply(out, top_k_weights, inv, offsets, k)
     assert result.shape[0] == num_tokens

@@ -16,6 +16,9 @@ enum { W_BF16 = 0, W_FP8 = 1, W_NF4 = 2 };
 struct GemmArgs {
   const bf16* x;
   int64_t ldx;
+  const int64_t* gather;  // NULL, or row r of the product is row gather[r] / gk of x (x has xrows rows)
+  int gk;
+  int64_t xrows;
   const uint8_t* w;      // bytes
   int64_t w_se, w_sk, w_sn;  // elements
   const float* scale;

@@ -575,7 +575,8 @@ using namespace mlora;
 
 static bool aligned(const void* p, uintptr_t n) { return ((uintptr_t)p & (n - 1)) == 0; }
 
-extern "C" int mlora_grouped_gemm(const void* x, int64_t ldx, int64_t rows, int K, int N, const void* w, int w_dtype,
+static int grouped_gemm_impl(const void* x, int64_t ldx, const int64_t* gather, int gk, int64_t xrows, int64_t rows,
+                             int K, int N, const void* w, int w_dtype,
                                   int64_t w_se, int64_t w_sk, int64_t w_sn, const float* scale, int scale_kind,
                                   int64_t scale_se, int scale_on_k, const uint8_t* nf4_absmax_q,
                                   const float* nf4_absmax2, const float* nf4_code2, const float* nf4_offset,
@@ -585,6 +586,11 @@ extern "C" int mlora_grouped_gemm(const void* x, int64_t ldx, int64_t rows, int 
                                   const int32_t* offsets, int E, void* stream) {
   clear_error();
   if (rows < 0) return fail("grouped_gemm: rows=%lld is negative", (long long)rows);
+  if (gather != nullptr) {
+    if (w_dtype != MLORA_DT_BF16) return fail("grouped_gemm_gather: gathered rows need a bf16 stack");
+    if (gk < 1) return fail("grouped_gemm_gather: k=%d must be >= 1", gk);
+    if (xrows < 0 || xrows * ldx * 2 > 0x7FFFFFF0) return fail("grouped_gemm_gather: x (%lld rows) exceeds 2 GiB", (long long)xrows);
+  }
   if (E < 1 || E > 4096) return fail("grouped_gemm: E=%d outside [1, 4096]", E);
   if (K < 8 || K % 8) return fail("grouped_gemm: K=%d must be a positive multiple of 8", K);
   if (N < 8 || N % 8) return fail("grouped_gemm: N=%d must be a positive multiple of 8", N);
@@ -635,6 +641,7 @@ extern "C" int mlora_grouped_gemm(const void* x, int64_t ldx, int64_t rows, int 
 
   GemmArgs g;
   g.x = (const bf16*)x; g.ldx = ldx;
+  g.gather = gather; g.gk = gk; g.xrows = xrows;
   g.w = (const uint8_t*)w; g.w_se = w_se; g.w_sk = w_sk; g.w_sn = w_sn;
   g.scale = scale; g.scale_se = scale_se; g.scale_kind = scale_kind;
   g.nf4_q = nf4_absmax_q; g.nf4_absmax2 = nf4_absmax2; g.nf4_code2 = nf4_code2; g.nf4_offset = nf4_offset;
@@ -655,4 +662,33 @@ extern "C" int mlora_grouped_gemm(const void* x, int64_t ldx, int64_t rows, int 
       return bkc ? launch_r<W_FP8, true, false>(g, s) : launch_r<W_FP8, false, false>(g, s);
     default: return bkc ? launch_r<W_NF4, true, false>(g, s) : launch_r<W_NF4, false, false>(g, s);
   }
+}
+
+extern "C" int mlora_grouped_gemm(const void* x, int64_t ldx, int64_t rows, int K, int N, const void* w, int w_dtype,
+                                  int64_t w_se, int64_t w_sk, int64_t w_sn, const float* scale, int scale_kind,
+                                  int64_t scale_se, int scale_on_k, const uint8_t* nf4_absmax_q,
+                                  const float* nf4_absmax2, const float* nf4_code2, const float* nf4_offset,
+                                  const float* nf4_code, const void* at, int64_t at_se, int64_t at_sr,
+                                  const void* bt, int64_t bt_se, int64_t bt_sn, int rank, float scaling,
+                                  const void* bias, int64_t bias_se, void* out, int64_t ldo, void* low, int64_t ldl,
+                                  const int32_t* offsets, int E, void* stream) {
+  return grouped_gemm_impl(x, ldx, nullptr, 1, rows, rows, K, N, w, w_dtype, w_se, w_sk, w_sn, scale, scale_kind,
+                           scale_se, scale_on_k, nf4_absmax_q, nf4_absmax2, nf4_code2, nf4_offset, nf4_code, at, at_se,
+                           at_sr, bt, bt_se, bt_sn, rank, scaling, bias, bias_se, out, ldo, low, ldl, offsets, E, stream);
+}
+
+extern "C" int mlora_grouped_gemm_gather(const void* x, int64_t ldx, int64_t x_rows, const int64_t* gather, int k,
+                                         int64_t rows, int K, int N, const void* w, int w_dtype, int64_t w_se,
+                                         int64_t w_sk, int64_t w_sn, const float* scale, int scale_kind,
+                                         int64_t scale_se, const void* at, int64_t at_se, int64_t at_sr,
+                                         const void* bt, int64_t bt_se, int64_t bt_sn, int rank, float scaling,
+                                         const void* bias, int64_t bias_se, void* out, int64_t ldo, void* low,
+                                         int64_t ldl, const int32_t* offsets, int E, void* stream) {
+  if (gather == nullptr) {
+    clear_error();
+    return fail("grouped_gemm_gather: gather is NULL");
+  }
+  return grouped_gemm_impl(x, ldx, gather, k, x_rows, rows, K, N, w, w_dtype, w_se, w_sk, w_sn, scale, scale_kind,
+                           scale_se, 0, nullptr, nullptr, nullptr, nullptr, nullptr, at, at_se, at_sr, bt, bt_se, bt_sn,
+                           rank, scaling, bias, bias_se, out, ldo, low, ldl, offsets, E, stream);
 }

@@ -169,12 +169,17 @@ struct Feed {
   bool a_on;
   int64_t wstep;           // bytes the stack offset advances per k (BKC: 2; else 2 * w_sk)
 
-  __device__ __forceinline__ void init(const GemmArgs& p, int n0, int wave, int lane) {
+  __device__ __forceinline__ void init(const GemmArgs& p, int n0, int64_t row0, int mrows, int wave, int lane) {
 #pragma unroll
     for (int q = 0; q < XI; ++q) {
       const int instr = wave * XI + q, ci = instr * 64 + lane;
       const int row = ci / CPR, c = (ci % CPR) ^ swz_f(row);
-      xo[q] = (uint32_t)((row * p.ldx + c * 8) * 2);
+      if (p.gather == nullptr) {
+        xo[q] = (uint32_t)((row * p.ldx + c * 8) * 2);
+      } else {  // the row's source row of x (x's resource spans all of x)
+        const int64_t src = row < mrows ? p.gather[row0 + row] / p.gk : -1;
+        xo[q] = src >= 0 ? (uint32_t)((src * p.ldx + c * 8) * 2) : kOob;
+      }
       xk[q] = c * 8;
       xd[q] = instr * 512;
     }
@@ -369,11 +374,12 @@ __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_ker
     const int an = min(FN, max(0, (nbk - wn + WAVES_N - 1) / WAVES_N));
 
     Feed<BKC, NRB> f;
-    f.rx = make_rsrc(p.x + row0 * p.ldx, (int64_t)mrows * p.ldx * 2);
+    f.rx = p.gather == nullptr ? make_rsrc(p.x + row0 * p.ldx, (int64_t)mrows * p.ldx * 2)
+                               : make_rsrc(p.x, p.xrows * p.ldx * 2);
     f.rw = make_rsrc(p.w + (int64_t)e * p.w_se * 2, p.w_se * 2);
     f.ra = f.rx;
     if constexpr (NRB > 0) f.ra = make_rsrc(p.at + (int64_t)e * p.at_se, (int64_t)RP * p.at_sr * 2);
-    f.init(p, n0, wave, lane);
+    f.init(p, n0, row0, mrows, wave, lane);
 
     f32x16 acc[FM][FN];
 #pragma unroll

@@ -23,6 +23,7 @@ __device__ __forceinline__ uint32_t hi2(uint32_t a, uint32_t b) { return __built
 
 template <int NRB>
 __global__ __launch_bounds__(256) void grouped_reduce_kernel(const bf16* __restrict__ g, int64_t ldg,
+                                                             const int64_t* __restrict__ gather, int gk,
                                                              const bf16* __restrict__ l, int64_t ldl, int64_t rows,
                                                              int N, float scaling, const int32_t* __restrict__ offsets,
                                                              bf16* __restrict__ out, int64_t o_se, int64_t o_sn,
@@ -47,7 +48,8 @@ __global__ __launch_bounds__(256) void grouped_reduce_kernel(const bf16* __restr
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
       const int64_t row = row0 + gr + q;
-      gv[q] = (row < end && g_cols) ? *(const u32x4*)(g + row * ldg + n0 + gc) : u32x4{0u, 0u, 0u, 0u};
+      const int64_t src = gather == nullptr || row >= end ? row : gather[row] / gk;  // g's row (gathered rows)
+      gv[q] = (row < end && g_cols) ? *(const u32x4*)(g + src * ldg + n0 + gc) : u32x4{0u, 0u, 0u, 0u};
       const int64_t lrow = row0 + lr + q;
       if (l_owner) lv[q] = lrow < end ? *(const u32x4*)(l + lrow * ldl + lc) : u32x4{0u, 0u, 0u, 0u};
     }
@@ -99,10 +101,11 @@ __global__ __launch_bounds__(256) void grouped_reduce_kernel(const bf16* __restr
 
 using namespace mlora;
 
-extern "C" int mlora_grouped_reduce(const void* g, int64_t ldg, const void* l, int64_t ldl, int64_t rows, int N, int R,
-                                    float scaling, const int32_t* offsets, int E, void* out, int64_t o_se,
-                                    int64_t o_sn, int64_t o_sr, void* stream) {
+static int grouped_reduce_impl(const void* g, int64_t ldg, const int64_t* gather, int gk, const void* l, int64_t ldl,
+                               int64_t rows, int N, int R, float scaling, const int32_t* offsets, int E, void* out,
+                               int64_t o_se, int64_t o_sn, int64_t o_sr, void* stream) {
   clear_error();
+  if (gather != nullptr && gk < 1) return fail("grouped_reduce_gather: k=%d must be >= 1", gk);
   if (E < 1 || E > 65535) return fail("grouped_reduce: E=%d outside [1, 65535]", E);
   if (N < 8 || N % 8 || ldg < N || ldg % 8 || ((uintptr_t)g & 15u))
     return fail("grouped_reduce: g needs N (%d) and its row stride (%lld) multiples of 8, 16-byte aligned", N, (long long)ldg);
@@ -111,7 +114,7 @@ extern "C" int mlora_grouped_reduce(const void* g, int64_t ldg, const void* l, i
   const dim3 grid((unsigned)E, (unsigned)((N + RB_N - 1) / RB_N)), block(256);
   hipStream_t s = as_stream(stream);
 #define MLORA_RED(NRB)                                                                                               \
-  hipLaunchKernelGGL(grouped_reduce_kernel<NRB>, grid, block, 0, s, (const bf16*)g, ldg, (const bf16*)l, ldl, rows, \
+  hipLaunchKernelGGL(grouped_reduce_kernel<NRB>, grid, block, 0, s, (const bf16*)g, ldg, gather, gk, (const bf16*)l, ldl, rows, \
                      N, scaling, offsets, (bf16*)out, o_se, o_sn, o_sr)
   switch (R / 16) {
     case 1: MLORA_RED(1); break;
@@ -121,4 +124,21 @@ extern "C" int mlora_grouped_reduce(const void* g, int64_t ldg, const void* l, i
   }
 #undef MLORA_RED
   return launch_status("grouped_reduce");
+}
+
+extern "C" int mlora_grouped_reduce(const void* g, int64_t ldg, const void* l, int64_t ldl, int64_t rows, int N, int R,
+                                    float scaling, const int32_t* offsets, int E, void* out, int64_t o_se,
+                                    int64_t o_sn, int64_t o_sr, void* stream) {
+  return grouped_reduce_impl(g, ldg, nullptr, 1, l, ldl, rows, N, R, scaling, offsets, E, out, o_se, o_sn, o_sr, stream);
+}
+
+extern "C" int mlora_grouped_reduce_gather(const void* g, int64_t ldg, const int64_t* gather, int k, const void* l,
+                                           int64_t ldl, int64_t rows, int N, int R, float scaling,
+                                           const int32_t* offsets, int E, void* out, int64_t o_se, int64_t o_sn,
+                                           int64_t o_sr, void* stream) {
+  if (gather == nullptr) {
+    clear_error();
+    return fail("grouped_reduce_gather: gather is NULL");
+  }
+  return grouped_reduce_impl(g, ldg, gather, k, l, ldl, rows, N, R, scaling, offsets, E, out, o_se, o_sn, o_sr, stream);
 }

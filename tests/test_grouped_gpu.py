@@ -273,3 +273,37 @@ def test_the_fp8_activation_pass_is_bit_exact(K, colscale):
     assert torch.equal(xs.cpu(), e8)
     low_ref = torch.einsum("rk,rjk->rj", xc.double(), at.cpu().double()[expert]).float()
     assert rel(low.float().cpu(), low_ref) < 1e-2
+
+
+@pytest.mark.parametrize("is_transposed", [False, True])
+def test_the_gathered_product_is_bit_identical_to_the_product_of_the_gathered_rows(is_transposed):
+    """lora_linear_gathered (rows read through perm, never materialised) against lora_linear on
+    hidden[perm // k]: the same tiles and the same sums, so the same bits, gradients included."""
+    from meepsquared_amd import _grouped, lora_linear, sort_by_expert
+    from meepsquared_amd._moe import _Gather
+
+    torch.manual_seed(5)
+    T, k, E, K, N, r = 300, 3, 6, 192, 160, 16
+    idx = torch.randint(0, E, (T, k), device="cuda")
+    idx[::11, 0] = E  # sentinel ids: rows after every expert
+    perm, inv, offsets = sort_by_expert(idx, E)
+    h = torch.randn(T, K, device="cuda", dtype=torch.bfloat16)
+    weight = torch.randn((E, K, N) if is_transposed else (E, N, K), device="cuda", dtype=torch.bfloat16) * 0.05
+    lhs, rhs = adapters(E, K, N, r, is_transposed)
+    bias = torch.randn(E, N, device="cuda", dtype=torch.bfloat16)
+    grad = torch.randn(T * k, N, device="cuda", dtype=torch.bfloat16)
+    live = int(offsets[-1])
+
+    h1 = h.clone().requires_grad_()
+    out1 = _grouped.lora_linear_gathered(h1, perm, inv, k, weight, None, offsets, is_transposed, lhs, rhs, 2.0, bias)
+    out1[:live].backward(grad[:live])
+    g1 = (out1[:live].detach().clone(), h1.grad.clone(), lhs.grad.clone(), rhs.grad.clone())
+    lhs.grad = rhs.grad = None
+
+    h2 = h.clone().requires_grad_()
+    sel = _Gather.apply(h2, perm, inv, offsets, k)  # the materialised rows, through the same gather kernel
+    out2 = lora_linear(sel, weight, None, offsets, is_transposed, lhs, rhs, 2.0, bias)
+    out2[:live].backward(grad[:live])
+    g2 = (out2[:live].detach(), h2.grad, lhs.grad, rhs.grad)
+    for name, a, b in zip(("out", "grad_h", "grad_lhs", "grad_rhs"), g1, g2):
+        assert torch.equal(a, b), name
