@@ -3,6 +3,7 @@
     python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline]
     python bench.py --copy-calibration MIB    # a plain device copy of known size, for PMC scaling
     python bench.py --config 3                # config 3: fp8 e4m3 stacks with per-row scales, fp8 MFMA
+    python bench.py --config 2|4              # Mixtral-shaped, Zipf-loaded / packed varlen batch, NF4 stacks
 
 A step is one forward and backward pass of the routed MoE-LoRA layer over one batch of synthetic
 inputs already resident in HBM: router top-k softmax (from given logits), counting sort, gather,
@@ -51,9 +52,35 @@ def gemm_launch_flops(info):
     return 2 * rows * (K * N + K * r + r * N)
 
 
-def make_inputs(device, seed=0):
+# the BASELINE configurations this bench can run (1 is the headline; 2-4 are reported beside it)
+CONFIGS = {
+    1: dict(T=T, H=H, I=I, E=E, k=K_TOP, r=R, alpha=ALPHA,
+            name="BASELINE config 1: Qwen3-30B-A3B-shaped MoE-LoRA layer fwd+bwd"),
+    2: dict(T=16384, H=4096, I=14336, E=8, k=2, r=16, alpha=32, zipf=1.2,
+            name="BASELINE config 2: Mixtral-8x7B-shaped MoE-LoRA layer fwd+bwd, Zipf(1.2)-loaded experts"),
+    3: dict(T=T, H=H, I=I, E=E, k=K_TOP, r=R, alpha=ALPHA, stack="fp8",
+            name="BASELINE config 3: config 1 with fp8-e4m3 stacks (per-row scales) on the fp8 MFMA"),
+    4: dict(H=H, I=I, E=E, k=K_TOP, r=R, alpha=ALPHA, stack="nf4", varlen=(64, 64, 2048),
+            name="BASELINE config 4: config 1 fed from a packed varlen batch (64 sequences, lengths U[64, 2048]), "
+                 "NF4 stacks (blocksize 64, double quant)"),
+}
+
+
+def config_tokens(c, seed=0):
+    """T of a configuration: fixed, or the total length of its packed varlen batch (seeded)."""
+    if "varlen" not in c:
+        return c["T"]
+    import numpy as np
+
+    n, lo, hi = c["varlen"]
+    return int(np.random.default_rng(seed).integers(lo, hi + 1, size=n).sum())
+
+
+def make_inputs(device, seed=0, c=None):
     import torch
 
+    c = c or CONFIGS[1]
+    T, H, I, E, R, ALPHA = config_tokens(c, seed), c["H"], c["I"], c["E"], c["r"], c["alpha"]
     g = torch.Generator(device=device).manual_seed(seed)
 
     def randn(*shape, std=1.0):
@@ -64,7 +91,10 @@ def make_inputs(device, seed=0):
 
     bf = torch.bfloat16
     hidden = randn(T, H).to(bf).requires_grad_()
-    logits = randn(T, E).to(bf)
+    logits = randn(T, E)
+    if "zipf" in c:  # router logits biased so that expert e's share of the load falls as (e + 1)^-s
+        logits = logits + (-c["zipf"] * torch.log(torch.arange(1, E + 1, device=device, dtype=torch.float32)))
+    logits = logits.to(bf)
     gate_up = randn(E, 2 * I, H, std=0.02).to(bf)
     down = randn(E, H, I, std=0.02).to(bf)
     s = ALPHA / R
@@ -121,6 +151,20 @@ def read_traffic():
     return None
 
 
+def roofline(c, achieved, config):
+    """The grouped product's achieved rate against the MFMA peak it runs on (traffic measured for config 1)."""
+    if c.get("stack") == "fp8":
+        return {"bound": "mfma", "kernel": "fp8_prep + fp8_gemm_kernel (4 products per step, timed together)",
+                "achieved": round(achieved, 2), "peak": PEAK_FP8_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(achieved / PEAK_FP8_TFLOPS, 4), "traffic": None}
+    kernel = ("grouped_gemm_kernel (register-staged, NF4 decoded in registers; 4 launches per step)"
+              if c.get("stack") == "nf4" else
+              "grouped_gemm_bf16_kernel (4 launches per step; traffic = mean HBM bytes per launch, rocprofv3 PMC)")
+    return {"bound": "mfma", "kernel": kernel, "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+            "traffic": read_traffic() if config == 1 else None}
+
+
 def copy_calibration(mib: int, reps: int = 3):
     """Copy a buffer of `mib` MiB device to device `reps` times: under rocprofv3 --pmc, FETCH_SIZE and
     WRITE_SIZE of these dispatches against the known byte count give the counters' scale factor."""
@@ -141,12 +185,13 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--cpu-tokens", type=int, default=T)
+    ap.add_argument("--cpu-tokens", type=int, default=CONFIGS[1]["T"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB")
-    ap.add_argument("--config", type=int, default=1, choices=(1, 3),
-                    help="1: the bf16 layer (default); 3: its stacks in fp8 e4m3 with one scale per output row, "
-                         "the products on the fp8 MFMA (activations quantised per row and 64 columns)")
+    ap.add_argument("--config", type=int, default=1, choices=(1, 2, 3, 4),
+                    help="1: the bf16 Qwen3-shaped layer (default, the headline); 2: Mixtral-shaped with Zipf-loaded "
+                         "experts; 3: config 1 with fp8 e4m3 stacks (per-row scales) on the fp8 MFMA; 4: config 1 "
+                         "shapes on a packed varlen batch with NF4 stacks")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {a.gpus})", file=sys.stderr)
@@ -162,8 +207,10 @@ def main():
     torch.backends.cuda.matmul.allow_tf32 = False
     device = "cuda:0"
     torch.cuda.set_device(0)
-    hidden, logits, gate_up, down, factors, dy = make_inputs(device)
-    if a.config == 3:
+    c = CONFIGS[a.config]
+    T, H, I, E, K_TOP, R = config_tokens(c), c["H"], c["I"], c["E"], c["k"], c["r"]
+    hidden, logits, gate_up, down, factors, dy = make_inputs(device, c=c)
+    if c.get("stack") == "fp8":
         from meepsquared_amd import _fp8
 
         gate_up8, gate_up_s = _fp8.quantize_stack(gate_up, per_row=True)
@@ -171,6 +218,11 @@ def main():
         del gate_up, down
         experts = Experts(gate_up8, down8, gate_up_proj_scale_inv=gate_up_s, down_proj_scale_inv=down_s)
         os.environ["MEEPSQUARED_FP8_PRODUCTS"] = "1"
+    elif c.get("stack") == "nf4":
+        from meepsquared_amd import _nf4
+
+        experts = Experts(_nf4.quantize_stack(gate_up), _nf4.quantize_stack(down))
+        del gate_up, down
     else:
         experts = Experts(gate_up, down)
     params = [hidden] + [t for (a_, b_, _) in factors.values() for t in (a_, b_)]
@@ -234,26 +286,28 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16" if a.config == 1 else "fp8-e4m3 products (bf16 activations, per-row fp32 stack scales)",
+        "dtype": {"fp8": "fp8-e4m3 products (bf16 activations, per-row fp32 stack scales)",
+                  "nf4": "bf16 products (NF4 stacks decoded in registers)"}.get(c.get("stack"), "bf16"),
         "data": "synthetic (seeded N(0,1) x and logits, N(0,0.02) W, Kaiming-uniform A, N(0,0.01) B)",
-        "config": {"workload": "BASELINE config 1: Qwen3-30B-A3B-shaped MoE-LoRA layer fwd+bwd" if a.config == 1 else
-                   "BASELINE config 3: config 1 with fp8-e4m3 stacks (per-row scales) on the fp8 MFMA",
-                   "tokens": T, "hidden": H, "moe_intermediate": I, "experts": E, "top_k": K_TOP,
-                   "lora_rank": R, "lora_alpha": ALPHA, "parallelism": "single GPU"},
+        "config": {"workload": c["name"], "tokens": T, "hidden": H, "moe_intermediate": I, "experts": E,
+                   "top_k": K_TOP, "lora_rank": R, "lora_alpha": c["alpha"], "parallelism": "single GPU"},
         "step_tflops": round(flops / (ms_per_step / 1e3) / 1e12, 2),
         "step_frac_of_bf16_peak": round(flops / (ms_per_step / 1e3) / 1e12 / PEAK_BF16_TFLOPS, 4),
-        "roofline": {"bound": "mfma", "kernel": "grouped_gemm_bf16_kernel (4 launches per step; traffic = mean HBM bytes per launch, rocprofv3 PMC)",
-                     "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": read_traffic()} if a.config == 1 else
-                    {"bound": "mfma", "kernel": "fp8_prep + fp8_gemm_kernel (4 products per step, timed together)",
-                     "achieved": round(achieved, 2), "peak": PEAK_FP8_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(achieved / PEAK_FP8_TFLOPS, 4), "traffic": None},
+        "roofline": roofline(c, achieved, a.config),
         "kernel_ms_per_step": {"grouped_gemm": round(gemm_ms / a.steps, 4),
                                "grouped_reduce": round(sum(ms for _, ms in red) / a.steps, 4),
                                "rest": round(ms_per_step - (gemm_ms + sum(ms for _, ms in red)) / a.steps, 4)},
         "grouped_gemm_ms_by_shape": {k_: round(sum(v) / len(v), 4) for k_, v in per_shape.items()},
         "wall_s_timed": round(wall, 3),
     }
+    if "zipf" in c or "varlen" in c:  # how ragged the expert groups were
+        counts = torch.bincount(topk_softmax(logits, K_TOP)[1].flatten(), minlength=E)
+        record["config"]["expert_rows"] = {"min": int(counts.min()), "max": int(counts.max()),
+                                           "mean": round(float(counts.float().mean()), 1)}
+        if "zipf" in c:
+            record["config"]["expert_rows"]["all"] = counts.tolist()
+        if "varlen" in c:
+            record["config"]["sequences"] = c["varlen"][0]
     if not a.no_cpu_baseline and a.config == 1:
         record["cpu_baseline"] = cpu_baseline(a.cpu_tokens)
     else:

@@ -11,11 +11,12 @@ from oracle import moe as ref_moe
 pytestmark = pytest.mark.gpu
 
 
-def make_layer(T, H, I, E, k, r, alpha, seed=0, is_transposed=False, sentinels=0.0):
-    """Config-0 style synthetic inputs: x, logits ~ N(0,1), W ~ N(0, 0.02), A Kaiming-uniform, B ~ N(0, 0.01)."""
+def make_layer(T, H, I, E, k, r, alpha, seed=0, is_transposed=False, zipf=0.0):
+    """Config-0 style synthetic inputs: x, logits ~ N(0,1), W ~ N(0, 0.02), A Kaiming-uniform, B ~ N(0, 0.01).
+    zipf > 0 biases the logits by -zipf * ln(e + 1), so that expert e's load falls roughly as (e + 1)^-zipf."""
     g = torch.Generator().manual_seed(seed)
     h = torch.randn(T, H, generator=g)
-    logits = torch.randn(T, E, generator=g)
+    logits = torch.randn(T, E, generator=g) - zipf * torch.log(torch.arange(1, E + 1, dtype=torch.float32))
     gu = torch.randn(E, 2 * I, H, generator=g) * 0.02
     dn = torch.randn(E, H, I, generator=g) * 0.02
     f = {"gate_up_proj": (torch.randn(E, 2 * I, r, generator=g) * 0.01, kaiming_uniform((E, r, H), H, g), alpha / r),
@@ -26,10 +27,11 @@ def make_layer(T, H, I, E, k, r, alpha, seed=0, is_transposed=False, sentinels=0
     return h, logits, gu, dn, f
 
 
-def run_layer(T, H, I, E, k, r, alpha, is_transposed=False, sentinel_frac=0.0, seed=0, fp8=None):
-    from meepsquared_amd import Experts, _fp8, routed_forward, topk_softmax
+def run_layer(T, H, I, E, k, r, alpha, is_transposed=False, sentinel_frac=0.0, seed=0, fp8=None, nf4=False,
+              zipf=0.0):
+    from meepsquared_amd import Experts, _fp8, _nf4, routed_forward, topk_softmax
 
-    h, logits, gu, dn, f = make_layer(T, H, I, E, k, r, alpha, seed, is_transposed)
+    h, logits, gu, dn, f = make_layer(T, H, I, E, k, r, alpha, seed, is_transposed, zipf)
     dev = "cuda"
     hb = h.to(dev, torch.bfloat16).requires_grad_()
     w, idx = topk_softmax(logits.to(dev, torch.bfloat16), k)
@@ -43,6 +45,8 @@ def run_layer(T, H, I, E, k, r, alpha, is_transposed=False, sentinel_frac=0.0, s
         gub, s1 = _fp8.quantize_stack(gub, per_row=fp8 == "row", is_transposed=is_transposed)
         dnb, s2 = _fp8.quantize_stack(dnb, per_row=fp8 == "row", is_transposed=is_transposed)
         scales = {"gate_up_proj": s1, "down_proj": s2}
+    if nf4:
+        gub, dnb = _nf4.quantize_stack(gub), _nf4.quantize_stack(dnb)
     experts = Experts(gub, dnb, is_transposed, scales.get("gate_up_proj"), scales.get("down_proj"))
     fb = {n: (a.to(dev, torch.bfloat16).requires_grad_(), b.to(dev, torch.bfloat16).requires_grad_(), s)
           for n, (a, b, s) in f.items()}
@@ -56,7 +60,10 @@ def run_layer(T, H, I, E, k, r, alpha, is_transposed=False, sentinel_frac=0.0, s
     # the oracle in float32 on the same (bf16-rounded) values, the fp8 stacks dequantised
     h32 = hb.detach().float().requires_grad_()
     w32 = w.detach().float().requires_grad_()
-    gu32, dn32 = gub.float(), dnb.float()
+    if nf4:  # the oracle runs on the stacks' decoded values
+        gu32, dn32 = _nf4.dequantize_stack(gub, torch.float32), _nf4.dequantize_stack(dnb, torch.float32)
+    else:
+        gu32, dn32 = gub.float(), dnb.float()
     f32 = {n: (a.detach().float().requires_grad_(), b.detach().float().requires_grad_(), s) for n, (a, b, s) in fb.items()}
     o32 = ref_moe.routed_forward(h32, idx, w32, gu32, dn32, f32, E, is_transposed, scales=scales)
     o32.backward(dy.float())
@@ -92,3 +99,19 @@ def test_qwen3_sized_layer_at_a_quarter_of_the_tokens():
     got, want = run_layer(2048, 2048, 768, 128, 8, 16, 32, seed=3)
     for name in want:
         assert rel(got[name], want[name]) < 1e-2, (name, rel(got[name], want[name]))
+
+
+def test_mixtral_shaped_layer_with_zipf_loaded_experts():
+    # config 2's routing (E=8, top-2, r=16, Zipf(1.2)-biased logits) at reduced width: the groups are ragged
+    got, want = run_layer(1024, 512, 1792, 8, 2, 16, 32, seed=5, zipf=1.2)
+    for name in want:
+        assert rel(got[name], want[name]) < 1e-2, (name, rel(got[name], want[name]))
+
+
+@pytest.mark.parametrize("is_transposed", [False, True])
+def test_layer_with_nf4_stacks_on_a_packed_varlen_batch(is_transposed):
+    # config 4: config-1 dims, NF4 stacks, the tokens of 6 packed sequences with lengths U[64, 512]
+    T = int(np.random.default_rng(4).integers(64, 513, size=6).sum())
+    got, want = run_layer(T, 2048, 768, 128, 8, 16, 32, is_transposed, seed=4, nf4=True)
+    for name in want:
+        assert rel(got[name], want[name]) < 3e-2, (name, rel(got[name], want[name]))
