@@ -271,10 +271,14 @@ def main():
     gemm_flops = sum(gemm_launch_flops(info) for info, _ in gemm)
     achieved = gemm_flops / (gemm_ms / 1e3) / 1e12
     flops = step_flops(T, H, I, K_TOP, R)
-    per_shape = {}
+    per_shape, red_shape = {}, {}
     for info, ms in gemm:
         key = f"{info['K']}->{info['N']}"
         per_shape.setdefault(key, []).append(ms)
+    for info, ms in red:
+        key = f"{info['N']}x{info['R']}" + ("/gathered" if info.get("gathered") else "") + \
+              ("/scaled" if info.get("scaled") else "")
+        red_shape.setdefault(key, []).append(ms)
     record = {
         "metric": "MoE-LoRA layer fwd+bwd tokens/sec; achieved TFLOP/s vs MFMA peak",
         "value": round(tokens_per_s, 1),
@@ -298,6 +302,7 @@ def main():
                                "grouped_reduce": round(sum(ms for _, ms in red) / a.steps, 4),
                                "rest": round(ms_per_step - (gemm_ms + sum(ms for _, ms in red)) / a.steps, 4)},
         "grouped_gemm_ms_by_shape": {k_: round(sum(v) / len(v), 4) for k_, v in per_shape.items()},
+        "grouped_reduce_ms_by_shape": {k_: round(sum(v) / len(v), 4) for k_, v in red_shape.items()},
         "wall_s_timed": round(wall, 3),
     }
     if "zipf" in c or "varlen" in c:  # how ragged the expert groups were

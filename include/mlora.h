@@ -122,9 +122,14 @@ int mlora_grouped_gemm(const void* x, int64_t ldx, int64_t rows, int K, int N,
 
 /* mlora_grouped_gemm with the rows of x gathered: row r of the product is row gather[r] / k of x
  * (x_rows rows, row stride ldx), so the expert-sorted copy h[perm // k] of the layer's input
- * (src/meepsquared/_moe.py:80) is never written.  bf16 stacks only; the other arguments as
- * mlora_grouped_gemm's (no per-row scale along k: the forward pass). */
-int mlora_grouped_gemm_gather(const void* x, int64_t ldx, int64_t x_rows, const int64_t* gather, int k, int64_t rows,
+ * (src/meepsquared/_moe.py:80) is never written.  With row_scale (MLORA_DT_BF16 or MLORA_DT_F32),
+ * output row r is (c · x W + scaling · bf16(x A) B) · row_scale[gather[r]] + bias: the input gradient
+ * of the down product straight from the layer's output gradient, the combine weights applied per row
+ * (src/meepsquared/_moe.py:123-126 and the down projection's backward, without the weighted copy of
+ * the gradient); low stays bf16(x A) of the unscaled rows.  bf16 stacks only; the other arguments
+ * as mlora_grouped_gemm's (no per-row stack scale along k). */
+int mlora_grouped_gemm_gather(const void* x, int64_t ldx, int64_t x_rows, const int64_t* gather, int k,
+                              const void* row_scale, int row_scale_dtype, int64_t rows,
                               int K, int N, const void* w, int w_dtype, int64_t w_se, int64_t w_sk, int64_t w_sn,
                               const float* scale, int scale_kind, int64_t scale_se,
                               const void* at, int64_t at_se, int64_t at_sr,
@@ -140,9 +145,14 @@ int mlora_grouped_reduce(const void* g, int64_t ldg, const void* l, int64_t ldl,
                          float scaling, const int32_t* offsets, int E,
                          void* out, int64_t o_se, int64_t o_sn, int64_t o_sr, void* stream);
 
-/* mlora_grouped_reduce with the rows of g gathered: row r is row gather[r] / k of g (A's gradient
- * of the gate_up product when its input rows are gathered, as mlora_grouped_gemm_gather reads them). */
-int mlora_grouped_reduce_gather(const void* g, int64_t ldg, const int64_t* gather, int k, const void* l, int64_t ldl,
+/* mlora_grouped_reduce with the rows of g gathered and/or weighted: with gather, row r is row
+ * gather[r] / k of g (A's gradient of the gate_up product when its input rows are gathered, as
+ * mlora_grouped_gemm_gather reads them); with row_scale, row r's term is weighted by
+ * row_scale[scale_index[r]], applied as bf16(row_scale[...] · l[r]) — for the down product's
+ * adapters, whose gradient rows the combine's backward (src/meepsquared/_moe.py:123-126) would have
+ * weighted.  At least one of gather and row_scale is given. */
+int mlora_grouped_reduce_gather(const void* g, int64_t ldg, const int64_t* gather, int k, const void* row_scale,
+                                int row_scale_dtype, const int64_t* scale_index, const void* l, int64_t ldl,
                                 int64_t rows, int N, int R, float scaling, const int32_t* offsets, int E,
                                 void* out, int64_t o_se, int64_t o_sn, int64_t o_sr, void* stream);
 
@@ -174,7 +184,8 @@ int mlora_combine(const void* y, int64_t H, const void* w, int w_dtype, const in
                   const int32_t* offsets, int E, void* out, void* stream);
 
 /* The combine's gradients: dy[inv[t*k+j], :] = bf16(dout[t, :] · w[t*k+j]) (zero for sentinel
- * rows) and dw[t*k+j] = sum_h dout[t, h] · y[inv[t*k+j], h] (zero for sentinel rows), in w_dtype. */
+ * rows) and dw[t*k+j] = sum_h dout[t, h] · y[inv[t*k+j], h] (zero for sentinel rows), in w_dtype.
+ * dy may be NULL (dw only: the down product then reads dout through mlora_grouped_gemm_gather). */
 int mlora_combine_backward(const void* dout, const void* y, int64_t H, const void* w, int w_dtype,
                            const int64_t* inv, int64_t T, int k, const int32_t* offsets, int E,
                            void* dy, void* dw, void* stream);

@@ -299,10 +299,11 @@ def _launch_fp8(x, weight, scale, offsets, is_transposed, adapters, scaling, bia
 
 
 def _reduce(g: torch.Tensor, low: torch.Tensor, offsets: torch.Tensor, scaling: float,
-            transposed: bool = False, gather=None) -> torch.Tensor:
+            transposed: bool = False, gather=None, row_scale=None) -> torch.Tensor:
     """(experts, N, R) bf16: scaling · sum over each expert's rows of g^T @ low (_grouped.py:362-370);
     (experts, R, N), written in that layout by the kernel, when transposed.  gather = (perm, k): the
-    rows are g[perm // k] (g then has its own row count)."""
+    rows are g[perm // k] (g then has its own row count).  row_scale = (w, index): row r's term
+    weighted by w[index[r]] (applied to low's row, rounded to bf16)."""
     experts = offsets.numel()
     N = g.shape[1]
     rows = low.shape[0] if gather is not None else g.shape[0]
@@ -315,15 +316,17 @@ def _reduce(g: torch.Tensor, low: torch.Tensor, offsets: torch.Tensor, scaling: 
     else:
         out = torch.empty((experts, N, R), device=g.device, dtype=torch.bfloat16)
         o_se, o_sn, o_sr = out.stride(0), out.stride(1), out.stride(2)
-    info = {"rows": rows, "N": N, "R": R}
+    info = {"rows": rows, "N": N, "R": R, "gathered": gather is not None, "scaled": row_scale is not None}
     if launch_observer is not None:
         launch_observer("grouped_reduce", "before", info)
-    if gather is None:
+    if gather is None and row_scale is None:
         call("mlora_grouped_reduce", ptr(g), g.stride(0), ptr(low), low.stride(0), rows, N, R, float(scaling),
              ptr(offsets), experts, ptr(out), o_se, o_sn, o_sr, _lib.stream(g.device))
     else:
-        perm, k = gather
-        call("mlora_grouped_reduce_gather", ptr(g), g.stride(0), ptr(perm), k, ptr(low), low.stride(0), rows, N, R,
+        perm, k = gather if gather is not None else (None, 1)
+        w, index = row_scale if row_scale is not None else (None, None)
+        call("mlora_grouped_reduce_gather", ptr(g), g.stride(0), ptr(perm), k, ptr(w),
+             _lib.dtype_code(w.dtype) if w is not None else 0, ptr(index), ptr(low), low.stride(0), rows, N, R,
              float(scaling), ptr(offsets), experts, ptr(out), o_se, o_sn, o_sr, _lib.stream(g.device))
     if launch_observer is not None:
         launch_observer("grouped_reduce", "after", info)
@@ -378,6 +381,41 @@ def gathered_product_fits(weight, products_fp8=None) -> bool:
     return isinstance(weight, torch.Tensor) and weight.dtype == torch.bfloat16 and not _x_fp8(weight, products_fp8)
 
 
+def _launch_gathered(src, perm, k, weight, scale, offsets, is_transposed, adapters, scaling, bias,
+                     row_scale=None, backward=False):
+    """One launch of the product over the rows src[perm // k] (bf16 stack): (out, low).  row_scale:
+    output row r multiplied by row_scale[perm[r]] (low stays bf16 of the unscaled rows' x·A)."""
+    _lib.require_gpu(src, perm, offsets, weight)
+    src = src if src.stride(-1) == 1 and src.stride(0) % 8 == 0 and src.data_ptr() % 16 == 0 else src.contiguous()
+    T, K = src.shape
+    rows = perm.numel()
+    N, w_se, w_sk, w_sn = _stack_strides(weight, K, is_transposed)
+    out = torch.empty((rows, N), device=src.device, dtype=torch.bfloat16)
+    R = adapters.padded if adapters is not None else 0
+    low = torch.empty((rows, R), device=src.device, dtype=torch.bfloat16) if adapters is not None else None
+    if rows == 0:
+        return out, low
+    scale_, scale_kind, scale_se, _ = _scale_args(scale, weight, backward)
+    if bias is not None:
+        bias = bias.to(torch.bfloat16)
+        bias = bias if bias.stride(-1) == 1 else bias.contiguous()
+    at, bt = (adapters.at, adapters.bt) if adapters is not None else (None, None)
+    info = {"rows": rows, "K": K, "N": N, "rank": adapters.rank if adapters is not None else 0}
+    if launch_observer is not None:
+        launch_observer("grouped_gemm", "before", info)
+    call("mlora_grouped_gemm_gather", ptr(src), src.stride(0), T, ptr(perm), k, ptr(row_scale),
+         _lib.dtype_code(row_scale.dtype) if row_scale is not None else 0, rows, K, N,
+         ptr(weight), _lib.DT_BF16, w_se, w_sk, w_sn, ptr(scale_), scale_kind, scale_se,
+         ptr(at), at.stride(0) if at is not None else 0, at.stride(1) if at is not None else 0,
+         ptr(bt), bt.stride(0) if bt is not None else 0, bt.stride(1) if bt is not None else 0,
+         R, float(scaling), ptr(bias), bias.stride(0) if bias is not None else 0,
+         ptr(out), out.stride(0), ptr(low), low.stride(0) if low is not None else 0,
+         ptr(offsets), offsets.numel(), _lib.stream(src.device))
+    if launch_observer is not None:
+        launch_observer("grouped_gemm", "after", info)
+    return out, low
+
+
 class _GatheredLoraProduct(torch.autograd.Function):
     """lora_linear of x = hidden[perm // k] without materialising x: the product and A's gradient read
     the rows of hidden through perm (the fusion of src/meepsquared/_moe.py:80 into the gate_up product).
@@ -388,32 +426,9 @@ class _GatheredLoraProduct(torch.autograd.Function):
         _lib.require_gpu(hidden, perm, offsets, weight)
         hidden = hidden if hidden.stride(-1) == 1 and hidden.stride(0) % 8 == 0 and hidden.data_ptr() % 16 == 0 \
             else hidden.contiguous()
-        T, K = hidden.shape
-        rows = perm.numel()
         offsets = offsets.to(torch.int32).contiguous()
         adapters = _Adapters(lhs, rhs, is_transposed) if lhs is not None else None
-        N, w_se, w_sk, w_sn = _stack_strides(weight, K, is_transposed)
-        out = torch.empty((rows, N), device=hidden.device, dtype=torch.bfloat16)
-        R = adapters.padded if adapters is not None else 0
-        low = torch.empty((rows, R), device=hidden.device, dtype=torch.bfloat16) if adapters is not None else None
-        if rows:
-            scale_, scale_kind, scale_se, _ = _scale_args(scale, weight, False)
-            if bias is not None:
-                bias = bias.to(torch.bfloat16)
-                bias = bias if bias.stride(-1) == 1 else bias.contiguous()
-            at, bt = (adapters.at, adapters.bt) if adapters is not None else (None, None)
-            info = {"rows": rows, "K": K, "N": N, "rank": adapters.rank if adapters is not None else 0}
-            if launch_observer is not None:
-                launch_observer("grouped_gemm", "before", info)
-            call("mlora_grouped_gemm_gather", ptr(hidden), hidden.stride(0), T, ptr(perm), k, rows, K, N,
-                 ptr(weight), _lib.DT_BF16, w_se, w_sk, w_sn, ptr(scale_), scale_kind, scale_se,
-                 ptr(at), at.stride(0) if at is not None else 0, at.stride(1) if at is not None else 0,
-                 ptr(bt), bt.stride(0) if bt is not None else 0, bt.stride(1) if bt is not None else 0,
-                 R, float(scaling), ptr(bias), bias.stride(0) if bias is not None else 0,
-                 ptr(out), out.stride(0), ptr(low), low.stride(0) if low is not None else 0,
-                 ptr(offsets), offsets.numel(), _lib.stream(hidden.device))
-            if launch_observer is not None:
-                launch_observer("grouped_gemm", "after", info)
+        out, low = _launch_gathered(hidden, perm, k, weight, scale, offsets, is_transposed, adapters, scaling, bias)
         ctx.save_for_backward(hidden, perm, inv, offsets, *((low,) if low is not None else ()))
         ctx.weight, ctx.adapters, ctx.scale = weight, adapters, scale
         ctx.is_transposed, ctx.scaling, ctx.k = is_transposed, scaling, k
@@ -448,6 +463,75 @@ class _GatheredLoraProduct(torch.autograd.Function):
         call("mlora_gather_rows_backward", ptr(grad_sel), K, ptr(inv), T, k, ptr(offsets), offsets.numel(),
              ptr(dh), _lib.stream(grad_out.device))
         return dh, None, None, None, None, None, None, None, grad_lhs, grad_rhs, None, None
+
+
+class _CombinedLoraProduct(torch.autograd.Function):
+    """combine(lora_linear(x, ...), weights): the down product and the weighted sum of each token's k
+    rows (src/meepsquared/_moe.py:88-126, the last product and :123-126).  The backward never writes
+    the weighted gradient rows bf16(w · dout[t]): the input-gradient product reads dout through perm and
+    multiplies each output row by its weight in the epilogue, and the adapters' reductions weight
+    each row's term as they load it.  Gradients for x, the weights and the adapters."""
+
+    @staticmethod
+    def forward(ctx, x, weights, perm, inv, k, weight, scale, offsets, is_transposed, lhs, rhs, scaling, bias):
+        offsets = offsets.to(torch.int32).contiguous()
+        adapters = _Adapters(lhs, rhs, is_transposed) if lhs is not None else None
+        y, low = _launch(x, weight, scale, offsets, is_transposed, adapters, scaling, bias, True)
+        S, H = y.shape
+        T = inv.numel() // k
+        w = weights.reshape(-1).contiguous()
+        if w.dtype not in (torch.bfloat16, torch.float32):
+            w = w.float()
+        out = torch.empty((T, H), device=y.device, dtype=y.dtype)
+        call("mlora_combine", ptr(y), H, ptr(w), _lib.dtype_code(w.dtype), ptr(inv), T, k, ptr(offsets),
+             offsets.numel(), ptr(out), _lib.stream(y.device))
+        ctx.save_for_backward(x, y, w, perm, inv, offsets, *((low,) if low is not None else ()))
+        ctx.weight, ctx.adapters, ctx.scale = weight, adapters, scale
+        ctx.is_transposed, ctx.scaling, ctx.k = is_transposed, scaling, k
+        ctx.lhs_dtype = lhs.dtype if lhs is not None else None
+        ctx.wshape, ctx.wdtype = weights.shape, weights.dtype
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        x, y, w, perm, inv, offsets, *rest = ctx.saved_tensors
+        adapters, weight, k = ctx.adapters, ctx.weight, ctx.k
+        dout = dout.to(torch.bfloat16).contiguous()
+        T, H = dout.shape
+        dw = torch.empty_like(w)
+        call("mlora_combine_backward", ptr(dout), ptr(y), H, ptr(w), _lib.dtype_code(w.dtype), ptr(inv), T, k,
+             ptr(offsets), offsets.numel(), None, ptr(dw), _lib.stream(dout.device))
+        grad_lhs = grad_rhs = None
+        if adapters is None:
+            grad_x, _ = _launch_gathered(dout, perm, k, weight, ctx.scale, offsets, not ctx.is_transposed, None, 1.0,
+                                         None, row_scale=w, backward=True)
+        else:
+            low = rest[0]
+            grad_x, low2 = _launch_gathered(dout, perm, k, weight, ctx.scale, offsets, not ctx.is_transposed,
+                                            adapters.swapped(), ctx.scaling, None, row_scale=w, backward=True)
+            rank = adapters.rank
+            ws = (w, perm)  # row r's weight: w[perm[r]]
+            if ctx.is_transposed:  # A = lhs (in, rank), B = rhs (rank, out)
+                grad_lhs = _reduce(x, low2, offsets, ctx.scaling, row_scale=ws)[:, :, :rank]
+                grad_rhs = _reduce(dout, low, offsets, ctx.scaling, transposed=True, gather=(perm, k),
+                                   row_scale=ws)[:, :rank, :]
+            else:  # A = rhs^T, B = lhs^T
+                grad_rhs = _reduce(x, low2, offsets, ctx.scaling, transposed=True, row_scale=ws)[:, :rank, :]
+                grad_lhs = _reduce(dout, low, offsets, ctx.scaling, gather=(perm, k), row_scale=ws)[:, :, :rank]
+            if ctx.lhs_dtype is not None and ctx.lhs_dtype != torch.bfloat16:
+                grad_lhs, grad_rhs = grad_lhs.to(ctx.lhs_dtype), grad_rhs.to(ctx.lhs_dtype)
+        dw = dw.view(ctx.wshape)
+        if dw.dtype != ctx.wdtype:
+            dw = dw.to(ctx.wdtype)
+        return grad_x, dw, None, None, None, None, None, None, None, grad_lhs, grad_rhs, None, None
+
+
+def lora_linear_combined(x, weights, perm, inv, k, weight, scale, offsets, is_transposed, lhs=None, rhs=None,
+                         scaling: float = 1.0, bias=None):
+    """combine(lora_linear(x, ...), weights) of the layer's down product (bf16 stacks), its backward
+    reading the output gradient through perm instead of a weighted copy of it."""
+    return _CombinedLoraProduct.apply(x, weights, perm, inv, k, weight, scale, offsets, is_transposed, lhs, rhs,
+                                      scaling, bias)
 
 
 def lora_linear_gathered(hidden, perm, inv, k, weight, scale, offsets, is_transposed, lhs=None, rhs=None,

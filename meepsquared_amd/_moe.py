@@ -214,8 +214,17 @@ def routed_forward(experts, hidden_states, top_k_index, top_k_weights, factors):
     else:
         gate_up = project(_Gather.apply(hidden_states, perm, inv, offsets, k), "gate_up_proj", "gate_up_proj_bias")
     act = _SwiGLU.apply(gate_up)
-    out = project(act, "down_proj", "down_proj_bias")
-    result = _Combine.apply(out, top_k_weights, inv, offsets, k)
+    if _grouped.gathered_product_fits(experts.down_proj):
+        # the down product and the combine as one Function: its backward reads the output gradient
+        # through perm, the combine weights applied per row, instead of a weighted copy of it
+        lhs, rhs, scaling = factors.get("down_proj", (None, None, 1.0))
+        bias = experts.down_proj_bias if getattr(experts, "has_bias", False) else None
+        result = _grouped.lora_linear_combined(act, top_k_weights, perm, inv, k, experts.down_proj,
+                                               _stack_scale(experts, "down_proj"), offsets, experts.is_transposed,
+                                               lhs, rhs, scaling, bias)
+    else:
+        out = project(act, "down_proj", "down_proj_bias")
+        result = _Combine.apply(out, top_k_weights, inv, offsets, k)
     assert result.shape[0] == num_tokens
     return result.to(hidden_states.dtype)
 

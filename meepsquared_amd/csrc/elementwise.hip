@@ -168,7 +168,7 @@ __global__ __launch_bounds__(256) void combine_backward_kernel(const u32x4* __re
           dot += d[q] * f[q];
         }
       }
-      dy[p * Hv + c] = pack8(o);
+      if (dy != nullptr) dy[p * Hv + c] = pack8(o);
     }
     dot = wave_sum(dot);
     if (lane == 0) part[wv] = dot;
@@ -297,6 +297,94 @@ __global__ __launch_bounds__(256) void transpose_kernel(const T* __restrict__ sr
   }
 }
 
+// The same for a narrow side (the adapters' rank, 16 or 32): a TA x TB tile of 4096 values, so that
+// every thread has work and each side's accesses run along its contiguous axis.
+template <typename T, int TA, int TB>
+__global__ __launch_bounds__(256) void transpose_narrow_kernel(const T* __restrict__ src, int64_t A, int64_t B,
+                                                               int64_t s_e, int64_t s_a, int64_t s_b,
+                                                               T* __restrict__ dst) {
+  static_assert(TA * TB == 4096, "one tile of 4096 values");
+  __shared__ T tile[TA][TB + 2];
+  const int64_t e = blockIdx.z, a0 = (int64_t)blockIdx.y * TA, b0 = (int64_t)blockIdx.x * TB;
+  const T* s = src + e * s_e;
+#pragma unroll 4
+  for (int idx = threadIdx.x; idx < TA * TB; idx += 256) {
+    const int i = idx / TB, j = idx % TB;
+    const int64_t a = a0 + i, b = b0 + j;
+    if (a < A && b < B) tile[i][j] = s[a * s_a + b * s_b];
+  }
+  __syncthreads();
+  T* d = dst + e * A * B;
+#pragma unroll 4
+  for (int idx = threadIdx.x; idx < TA * TB; idx += 256) {
+    const int j = idx / TA, i = idx % TA;
+    const int64_t a = a0 + i, b = b0 + j;
+    if (a < A && b < B) d[b * A + a] = tile[i][j];
+  }
+}
+
+// The narrow-side transpose with 16-byte accesses on both sides (bf16, both sizes multiples of 8,
+// the source contiguous along b): rows of the source are read as vectors into a TA x TB tile,
+// columns of the tile are gathered eight at a time and written as vectors along a.
+template <int TA, int TB>
+__global__ __launch_bounds__(256) void transpose_vec_kernel(const bf16* __restrict__ src, int64_t A, int64_t B,
+                                                            int64_t s_e, int64_t s_a, bf16* __restrict__ dst) {
+  static_assert(TA * TB == 4096 && TA % 8 == 0 && TB % 8 == 0, "a tile of 4096 values in vectors of 8");
+  __shared__ __attribute__((aligned(16))) bf16 tile[TA][TB + 8];
+  constexpr int NV = TA * TB / 8;
+  const int64_t e = blockIdx.z, a0 = (int64_t)blockIdx.y * TA, b0 = (int64_t)blockIdx.x * TB;
+  const bf16* s = src + e * s_e;
+#pragma unroll
+  for (int v = threadIdx.x; v < NV; v += 256) {
+    const int i = v / (TB / 8), j = (v % (TB / 8)) * 8;
+    const int64_t a = a0 + i, b = b0 + j;
+    u32x4 val = {0u, 0u, 0u, 0u};
+    if (a < A && b < B) val = *(const u32x4*)(s + a * s_a + b);
+    *(u32x4*)&tile[i][j] = val;
+  }
+  __syncthreads();
+  bf16* d = dst + e * A * B;
+#pragma unroll
+  for (int v = threadIdx.x; v < NV; v += 256) {
+    const int j = v / (TA / 8), i = (v % (TA / 8)) * 8;  // column j, rows i .. i + 7
+    const int64_t a = a0 + i, b = b0 + j;
+    if (a < A && b < B) {
+      u32x4 o;
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        o[q] = (uint32_t)__builtin_bit_cast(uint16_t, tile[i + 2 * q][j]) |
+               ((uint32_t)__builtin_bit_cast(uint16_t, tile[i + 2 * q + 1][j]) << 16);
+      *(u32x4*)(d + b * A + a) = o;
+    }
+  }
+}
+
+template <int TA, int TB>
+static int launch_transpose_vec(const void* src, int64_t E, int64_t A, int64_t B, int64_t s_e, int64_t s_a,
+                                void* dst, void* stream) {
+  if (E > 65535 || (A + TA - 1) / TA > 65535 || (B + TB - 1) / TB > 0x7FFFFFFF)
+    return fail("transpose: (E=%lld, A=%lld, B=%lld) exceeds the grid", (long long)E, (long long)A, (long long)B);
+  const dim3 grid((unsigned)((B + TB - 1) / TB), (unsigned)((A + TA - 1) / TA), (unsigned)E);
+  hipLaunchKernelGGL((transpose_vec_kernel<TA, TB>), grid, dim3(256), 0, as_stream(stream), (const bf16*)src, A, B,
+                     s_e, s_a, (bf16*)dst);
+  return launch_status("transpose");
+}
+
+template <typename T, int TA, int TB>
+static int launch_transpose(const char* what, const void* src, int64_t E, int64_t A, int64_t B, int64_t s_e,
+                            int64_t s_a, int64_t s_b, void* dst, void* stream) {
+  if (E > 65535 || (A + TA - 1) / TA > 65535 || (B + TB - 1) / TB > 0x7FFFFFFF)
+    return fail("%s: (E=%lld, A=%lld, B=%lld) exceeds the grid", what, (long long)E, (long long)A, (long long)B);
+  const dim3 grid((unsigned)((B + TB - 1) / TB), (unsigned)((A + TA - 1) / TA), (unsigned)E);
+  if constexpr (TA == 64 && TB == 64)
+    hipLaunchKernelGGL(transpose_kernel<T>, grid, dim3(256), 0, as_stream(stream), (const T*)src, A, B, s_e, s_a, s_b,
+                       (T*)dst);
+  else
+    hipLaunchKernelGGL((transpose_narrow_kernel<T, TA, TB>), grid, dim3(256), 0, as_stream(stream), (const T*)src, A,
+                       B, s_e, s_a, s_b, (T*)dst);
+  return launch_status(what);
+}
+
 }  // namespace mlora
 
 extern "C" int mlora_transpose(const void* src, int64_t E, int64_t A, int64_t B, int64_t s_e, int64_t s_a,
@@ -304,11 +392,18 @@ extern "C" int mlora_transpose(const void* src, int64_t E, int64_t A, int64_t B,
   clear_error();
   if (E < 0 || A < 0 || B < 0) return fail("transpose: negative size");
   if (E == 0 || A == 0 || B == 0) return 0;
-  if (E > 65535 || (A + 63) / 64 > 65535 || (B + 63) / 64 > 0x7FFFFFFF)
-    return fail("transpose: (E=%lld, A=%lld, B=%lld) exceeds the grid", (long long)E, (long long)A, (long long)B);
-  hipLaunchKernelGGL(transpose_kernel<bf16>, dim3((unsigned)((B + 63) / 64), (unsigned)((A + 63) / 64), (unsigned)E),
-                     dim3(256), 0, as_stream(stream), (const bf16*)src, A, B, s_e, s_a, s_b, (bf16*)dst);
-  return launch_status("transpose");
+  const bool vec = s_b == 1 && A % 8 == 0 && B % 8 == 0 && s_a % 8 == 0 && s_e % 8 == 0 && ((uintptr_t)src & 15u) == 0 &&
+                   ((uintptr_t)dst & 15u) == 0;
+  if (vec && A <= 16 && B > 16) return launch_transpose_vec<16, 256>(src, E, A, B, s_e, s_a, dst, stream);
+  if (vec && B <= 16 && A > 16) return launch_transpose_vec<256, 16>(src, E, A, B, s_e, s_a, dst, stream);
+  if (vec && A <= 32 && B > 32) return launch_transpose_vec<32, 128>(src, E, A, B, s_e, s_a, dst, stream);
+  if (vec && B <= 32 && A > 32) return launch_transpose_vec<128, 32>(src, E, A, B, s_e, s_a, dst, stream);
+  if (vec) return launch_transpose_vec<64, 64>(src, E, A, B, s_e, s_a, dst, stream);
+  if (A <= 16 && B > 16) return launch_transpose<bf16, 16, 256>("transpose", src, E, A, B, s_e, s_a, s_b, dst, stream);
+  if (B <= 16 && A > 16) return launch_transpose<bf16, 256, 16>("transpose", src, E, A, B, s_e, s_a, s_b, dst, stream);
+  if (A <= 32 && B > 32) return launch_transpose<bf16, 32, 128>("transpose", src, E, A, B, s_e, s_a, s_b, dst, stream);
+  if (B <= 32 && A > 32) return launch_transpose<bf16, 128, 32>("transpose", src, E, A, B, s_e, s_a, s_b, dst, stream);
+  return launch_transpose<bf16, 64, 64>("transpose", src, E, A, B, s_e, s_a, s_b, dst, stream);
 }
 
 extern "C" int mlora_transpose_u8(const void* src, int64_t E, int64_t A, int64_t B, int64_t s_e, int64_t s_a,

@@ -613,7 +613,7 @@ extern "C" int mlora_fp8_gemm(const void* x8, int64_t ld8, const int32_t* xs, in
   if (rows == 0) return 0;
   f8::Args a;
   GemmArgs& g = a.g;
-  g.x = nullptr; g.ldx = 0; g.gather = nullptr; g.gk = 1; g.xrows = 0;
+  g.x = nullptr; g.ldx = 0; g.gather = nullptr; g.gk = 1; g.xrows = 0; g.row_scale = nullptr; g.row_scale_dt = 0;
   g.w = (const uint8_t*)w; g.w_se = w_se; g.w_sk = 1; g.w_sn = w_sn;
   g.scale = scale; g.scale_se = scale_se; g.scale_kind = scale_kind;
   g.nf4_q = nullptr; g.nf4_absmax2 = nullptr; g.nf4_code2 = nullptr; g.nf4_offset = nullptr; g.nf4_code = nullptr;

@@ -19,6 +19,8 @@ struct GemmArgs {
   const int64_t* gather;  // NULL, or row r of the product is row gather[r] / gk of x (x has xrows rows)
   int gk;
   int64_t xrows;
+  const void* row_scale;  // NULL, or (with gather) output row r is multiplied by row_scale[gather[r]]
+  int row_scale_dt;       // MLORA_DT_BF16 or MLORA_DT_F32
   const uint8_t* w;      // bytes
   int64_t w_se, w_sk, w_sn;  // elements
   const float* scale;

@@ -575,8 +575,9 @@ using namespace mlora;
 
 static bool aligned(const void* p, uintptr_t n) { return ((uintptr_t)p & (n - 1)) == 0; }
 
-static int grouped_gemm_impl(const void* x, int64_t ldx, const int64_t* gather, int gk, int64_t xrows, int64_t rows,
-                             int K, int N, const void* w, int w_dtype,
+static int grouped_gemm_impl(const void* x, int64_t ldx, const int64_t* gather, int gk, int64_t xrows,
+                             const void* row_scale, int row_scale_dt, int64_t rows, int K, int N, const void* w,
+                             int w_dtype,
                                   int64_t w_se, int64_t w_sk, int64_t w_sn, const float* scale, int scale_kind,
                                   int64_t scale_se, int scale_on_k, const uint8_t* nf4_absmax_q,
                                   const float* nf4_absmax2, const float* nf4_code2, const float* nf4_offset,
@@ -590,6 +591,11 @@ static int grouped_gemm_impl(const void* x, int64_t ldx, const int64_t* gather, 
     if (w_dtype != MLORA_DT_BF16) return fail("grouped_gemm_gather: gathered rows need a bf16 stack");
     if (gk < 1) return fail("grouped_gemm_gather: k=%d must be >= 1", gk);
     if (xrows < 0 || xrows * ldx * 2 > 0x7FFFFFF0) return fail("grouped_gemm_gather: x (%lld rows) exceeds 2 GiB", (long long)xrows);
+  }
+  if (row_scale != nullptr) {
+    if (gather == nullptr) return fail("grouped_gemm: a row scale is indexed through gather");
+    if (row_scale_dt != MLORA_DT_BF16 && row_scale_dt != MLORA_DT_F32)
+      return fail("grouped_gemm_gather: row scale dtype %d is not bf16/f32", row_scale_dt);
   }
   if (E < 1 || E > 4096) return fail("grouped_gemm: E=%d outside [1, 4096]", E);
   if (K < 8 || K % 8) return fail("grouped_gemm: K=%d must be a positive multiple of 8", K);
@@ -642,6 +648,7 @@ static int grouped_gemm_impl(const void* x, int64_t ldx, const int64_t* gather, 
   GemmArgs g;
   g.x = (const bf16*)x; g.ldx = ldx;
   g.gather = gather; g.gk = gk; g.xrows = xrows;
+  g.row_scale = row_scale; g.row_scale_dt = row_scale_dt;
   g.w = (const uint8_t*)w; g.w_se = w_se; g.w_sk = w_sk; g.w_sn = w_sn;
   g.scale = scale; g.scale_se = scale_se; g.scale_kind = scale_kind;
   g.nf4_q = nf4_absmax_q; g.nf4_absmax2 = nf4_absmax2; g.nf4_code2 = nf4_code2; g.nf4_offset = nf4_offset;
@@ -672,13 +679,14 @@ extern "C" int mlora_grouped_gemm(const void* x, int64_t ldx, int64_t rows, int 
                                   const void* bt, int64_t bt_se, int64_t bt_sn, int rank, float scaling,
                                   const void* bias, int64_t bias_se, void* out, int64_t ldo, void* low, int64_t ldl,
                                   const int32_t* offsets, int E, void* stream) {
-  return grouped_gemm_impl(x, ldx, nullptr, 1, rows, rows, K, N, w, w_dtype, w_se, w_sk, w_sn, scale, scale_kind,
+  return grouped_gemm_impl(x, ldx, nullptr, 1, rows, nullptr, 0, rows, K, N, w, w_dtype, w_se, w_sk, w_sn, scale,
+                           scale_kind,
                            scale_se, scale_on_k, nf4_absmax_q, nf4_absmax2, nf4_code2, nf4_offset, nf4_code, at, at_se,
                            at_sr, bt, bt_se, bt_sn, rank, scaling, bias, bias_se, out, ldo, low, ldl, offsets, E, stream);
 }
 
 extern "C" int mlora_grouped_gemm_gather(const void* x, int64_t ldx, int64_t x_rows, const int64_t* gather, int k,
-                                         int64_t rows, int K, int N, const void* w, int w_dtype, int64_t w_se,
+                                         const void* row_scale, int row_scale_dtype, int64_t rows, int K, int N, const void* w, int w_dtype, int64_t w_se,
                                          int64_t w_sk, int64_t w_sn, const float* scale, int scale_kind,
                                          int64_t scale_se, const void* at, int64_t at_se, int64_t at_sr,
                                          const void* bt, int64_t bt_se, int64_t bt_sn, int rank, float scaling,
@@ -688,7 +696,8 @@ extern "C" int mlora_grouped_gemm_gather(const void* x, int64_t ldx, int64_t x_r
     clear_error();
     return fail("grouped_gemm_gather: gather is NULL");
   }
-  return grouped_gemm_impl(x, ldx, gather, k, x_rows, rows, K, N, w, w_dtype, w_se, w_sk, w_sn, scale, scale_kind,
+  return grouped_gemm_impl(x, ldx, gather, k, x_rows, row_scale, row_scale_dtype, rows, K, N, w, w_dtype, w_se, w_sk,
+                           w_sn, scale, scale_kind,
                            scale_se, 0, nullptr, nullptr, nullptr, nullptr, nullptr, at, at_se, at_sr, bt, bt_se, bt_sn,
                            rank, scaling, bias, bias_se, out, ldo, low, ldl, offsets, E, stream);
 }

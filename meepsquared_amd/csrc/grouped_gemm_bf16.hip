@@ -2,6 +2,8 @@
 //
 //   out_e = c · x_e W_e + scaling · bf16(x_e A_e) B_e + bias_e         for every expert e
 //
+// (with gathered rows, each output row may be multiplied by a per-row scale before the bias)
+//
 // Same work decomposition as the register-staged kernel (grouped_gemm.hip): a persistent grid,
 // each workgroup deriving the tile map in LDS, items split into one contiguous range per XCD.
 // What differs is how operands reach LDS and how deep the pipeline is:
@@ -460,6 +462,11 @@ __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_ker
       const int row = (i * WAVES_M + wm) * 32 + (lane & 31);
       if (i >= am) continue;
       bf16* orow = p.out + (row0 + row) * p.ldo;
+      float rs = 1.f;  // the row's output scale (the combine weight of a gathered gradient row)
+      if (p.row_scale != nullptr && row < mrows) {
+        const int64_t si = p.gather[row0 + row];
+        rs = p.row_scale_dt == MLORA_DT_F32 ? ((const float*)p.row_scale)[si] : (float)((const bf16*)p.row_scale)[si];
+      }
 #pragma unroll
       for (int j = 0; j < FN; ++j) {
         if (j >= an) continue;
@@ -486,7 +493,8 @@ __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_ker
           }
           float o[4];
 #pragma unroll
-          for (int q = 0; q < 4; ++q) o[q] = acc[i][j][4 * g + q] * cs[j][g][q] + p.scaling * t[4 * g + q] + bias[q];
+          for (int q = 0; q < 4; ++q)
+            o[q] = (acc[i][j][4 * g + q] * cs[j][g][q] + p.scaling * t[4 * g + q]) * rs + bias[q];
           u32x2 v;
           v[0] = pack_bf16x2(o[0], o[1]);
           v[1] = pack_bf16x2(o[2], o[3]);

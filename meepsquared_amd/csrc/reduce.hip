@@ -9,13 +9,17 @@
 // registers while the current one is multiplied.  Every output element has exactly one writer
 // and a fixed summation order: no atomics, the same bits every run.
 //
+// Rows of g may be gathered (row r read from g[gather[r] / gk]) and weighted by a per-row scale,
+// applied to the narrow operand: row r of l taken as bf16(row_scale[scale_index[r]] · l[r]).
+//
 // Reference behaviour: src/meepsquared/_grouped.py:232-256 (_grouped_reduce_kernel), :362-370 (_reduce).
 #include "common.hpp"
 
 namespace mlora {
 
-constexpr int RB_N = 64;     // columns of g per workgroup
-constexpr int RB_ROWS = 64;  // rows per slice
+constexpr int RB_N = 64;  // columns of g per workgroup
+constexpr int RPT = 2;                 // rows of g each thread loads per slice
+constexpr int RB_ROWS = 32 * RPT;      // rows per slice
 constexpr int RP_ = RB_ROWS + 8;
 
 __device__ __forceinline__ uint32_t lo2(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x05040100u); }
@@ -24,6 +28,8 @@ __device__ __forceinline__ uint32_t hi2(uint32_t a, uint32_t b) { return __built
 template <int NRB>
 __global__ __launch_bounds__(256) void grouped_reduce_kernel(const bf16* __restrict__ g, int64_t ldg,
                                                              const int64_t* __restrict__ gather, int gk,
+                                                             const void* __restrict__ row_scale, int rs_dt,
+                                                             const int64_t* __restrict__ rs_idx,
                                                              const bf16* __restrict__ l, int64_t ldl, int64_t rows,
                                                              int N, float scaling, const int32_t* __restrict__ offsets,
                                                              bf16* __restrict__ out, int64_t o_se, int64_t o_sn,
@@ -37,34 +43,55 @@ __global__ __launch_bounds__(256) void grouped_reduce_kernel(const bf16* __restr
   const int64_t start = e == 0 ? 0 : min(max((int64_t)offsets[e - 1], (int64_t)0), rows);
   const int64_t end = min(max((int64_t)offsets[e], (int64_t)0), rows);
 
-  // this thread's 2 rows x 8 columns of g, and (threads < 32 * R/8) 2 rows x 8 ranks of l
-  const int gr = (tid >> 3) * 2, gc = (tid & 7) * 8;
-  const int lr = (tid / (R / 8)) * 2, lc = (tid % (R / 8)) * 8;
-  const bool l_owner = tid < 32 * (R / 8);
+  // this thread's RPT rows x 8 columns of g; the 4R threads that copy l (RPT rows x 8 ranks each)
+  // are spread over the waves where 256 divides evenly
+  constexpr int LSTRIDE = 256 % (4 * R) == 0 ? 256 / (4 * R) : 1;
+  const int gr = (tid >> 3) * RPT, gc = (tid & 7) * 8;
+  const int lo = tid / LSTRIDE;
+  const int lr = (lo / (R / 8)) * RPT, lc = (lo % (R / 8)) * 8;
+  const bool l_owner = tid % LSTRIDE == 0 && lo < 4 * R;
   const bool g_cols = n0 + gc < N;
 
-  u32x4 gv[2], lv[2];
+  u32x4 gv[RPT], lv[RPT];
+  float ws[RPT];
+#pragma unroll
+  for (int q = 0; q < RPT; ++q) ws[q] = 1.f;
   auto load = [&](int64_t row0) {
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
+    for (int q = 0; q < RPT; ++q) {
       const int64_t row = row0 + gr + q;
       const int64_t src = gather == nullptr || row >= end ? row : gather[row] / gk;  // g's row (gathered rows)
       gv[q] = (row < end && g_cols) ? *(const u32x4*)(g + src * ldg + n0 + gc) : u32x4{0u, 0u, 0u, 0u};
       const int64_t lrow = row0 + lr + q;
-      if (l_owner) lv[q] = lrow < end ? *(const u32x4*)(l + lrow * ldl + lc) : u32x4{0u, 0u, 0u, 0u};
+      if (l_owner) {
+        lv[q] = lrow < end ? *(const u32x4*)(l + lrow * ldl + lc) : u32x4{0u, 0u, 0u, 0u};
+        if (row_scale != nullptr && lrow < end) {
+          const int64_t si = rs_idx[lrow];
+          ws[q] = rs_dt == MLORA_DT_F32 ? ((const float*)row_scale)[si] : (float)((const bf16*)row_scale)[si];
+        }
+      }
     }
   };
   auto store = [&]() {
-    // transpose 2 rows x 8 columns into 8 columns x 2 rows
+    if (row_scale != nullptr && l_owner) {  // l's rows weighted here, after the loads have had the MFMAs to land
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      *(uint32_t*)(Gs + (gc + 2 * m) * RP_ + gr) = lo2(gv[0][m], gv[1][m]);
-      *(uint32_t*)(Gs + (gc + 2 * m + 1) * RP_ + gr) = hi2(gv[0][m], gv[1][m]);
-      if (l_owner) {
-        *(uint32_t*)(Ls + (lc + 2 * m) * RP_ + lr) = lo2(lv[0][m], lv[1][m]);
-        *(uint32_t*)(Ls + (lc + 2 * m + 1) * RP_ + lr) = hi2(lv[0][m], lv[1][m]);
-      }
+      for (int q = 0; q < RPT; ++q)
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+          lv[q][m] = pack_bf16x2(bf16_bits_to_f32(lv[q][m] & 0xFFFFu) * ws[q], bf16_bits_to_f32(lv[q][m] >> 16) * ws[q]);
     }
+    // transpose RPT rows x 8 columns into 8 columns x RPT rows, two rows per 32-bit store
+#pragma unroll
+    for (int pr = 0; pr < RPT; pr += 2)
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        *(uint32_t*)(Gs + (gc + 2 * m) * RP_ + gr + pr) = lo2(gv[pr][m], gv[pr + 1][m]);
+        *(uint32_t*)(Gs + (gc + 2 * m + 1) * RP_ + gr + pr) = hi2(gv[pr][m], gv[pr + 1][m]);
+        if (l_owner) {
+          *(uint32_t*)(Ls + (lc + 2 * m) * RP_ + lr + pr) = lo2(lv[pr][m], lv[pr + 1][m]);
+          *(uint32_t*)(Ls + (lc + 2 * m + 1) * RP_ + lr + pr) = hi2(lv[pr][m], lv[pr + 1][m]);
+        }
+      }
   };
 
   f32x4 acc[NRB];
@@ -101,11 +128,14 @@ __global__ __launch_bounds__(256) void grouped_reduce_kernel(const bf16* __restr
 
 using namespace mlora;
 
-static int grouped_reduce_impl(const void* g, int64_t ldg, const int64_t* gather, int gk, const void* l, int64_t ldl,
-                               int64_t rows, int N, int R, float scaling, const int32_t* offsets, int E, void* out,
-                               int64_t o_se, int64_t o_sn, int64_t o_sr, void* stream) {
+static int grouped_reduce_impl(const void* g, int64_t ldg, const int64_t* gather, int gk, const void* row_scale,
+                               int rs_dt, const int64_t* rs_idx, const void* l, int64_t ldl, int64_t rows, int N, int R,
+                               float scaling, const int32_t* offsets, int E, void* out, int64_t o_se, int64_t o_sn,
+                               int64_t o_sr, void* stream) {
   clear_error();
   if (gather != nullptr && gk < 1) return fail("grouped_reduce_gather: k=%d must be >= 1", gk);
+  if (row_scale != nullptr && (rs_idx == nullptr || (rs_dt != MLORA_DT_BF16 && rs_dt != MLORA_DT_F32)))
+    return fail("grouped_reduce_gather: a row scale needs its index and a bf16/f32 dtype (got %d)", rs_dt);
   if (E < 1 || E > 65535) return fail("grouped_reduce: E=%d outside [1, 65535]", E);
   if (N < 8 || N % 8 || ldg < N || ldg % 8 || ((uintptr_t)g & 15u))
     return fail("grouped_reduce: g needs N (%d) and its row stride (%lld) multiples of 8, 16-byte aligned", N, (long long)ldg);
@@ -114,8 +144,8 @@ static int grouped_reduce_impl(const void* g, int64_t ldg, const int64_t* gather
   const dim3 grid((unsigned)E, (unsigned)((N + RB_N - 1) / RB_N)), block(256);
   hipStream_t s = as_stream(stream);
 #define MLORA_RED(NRB)                                                                                               \
-  hipLaunchKernelGGL(grouped_reduce_kernel<NRB>, grid, block, 0, s, (const bf16*)g, ldg, gather, gk, (const bf16*)l, ldl, rows, \
-                     N, scaling, offsets, (bf16*)out, o_se, o_sn, o_sr)
+  hipLaunchKernelGGL(grouped_reduce_kernel<NRB>, grid, block, 0, s, (const bf16*)g, ldg, gather, gk, row_scale, rs_dt,   \
+                     rs_idx, (const bf16*)l, ldl, rows, N, scaling, offsets, (bf16*)out, o_se, o_sn, o_sr)
   switch (R / 16) {
     case 1: MLORA_RED(1); break;
     case 2: MLORA_RED(2); break;
@@ -129,16 +159,19 @@ static int grouped_reduce_impl(const void* g, int64_t ldg, const int64_t* gather
 extern "C" int mlora_grouped_reduce(const void* g, int64_t ldg, const void* l, int64_t ldl, int64_t rows, int N, int R,
                                     float scaling, const int32_t* offsets, int E, void* out, int64_t o_se,
                                     int64_t o_sn, int64_t o_sr, void* stream) {
-  return grouped_reduce_impl(g, ldg, nullptr, 1, l, ldl, rows, N, R, scaling, offsets, E, out, o_se, o_sn, o_sr, stream);
+  return grouped_reduce_impl(g, ldg, nullptr, 1, nullptr, 0, nullptr, l, ldl, rows, N, R, scaling, offsets, E, out,
+                             o_se, o_sn, o_sr, stream);
 }
 
-extern "C" int mlora_grouped_reduce_gather(const void* g, int64_t ldg, const int64_t* gather, int k, const void* l,
-                                           int64_t ldl, int64_t rows, int N, int R, float scaling,
+extern "C" int mlora_grouped_reduce_gather(const void* g, int64_t ldg, const int64_t* gather, int k,
+                                           const void* row_scale, int row_scale_dtype, const int64_t* scale_index,
+                                           const void* l, int64_t ldl, int64_t rows, int N, int R, float scaling,
                                            const int32_t* offsets, int E, void* out, int64_t o_se, int64_t o_sn,
                                            int64_t o_sr, void* stream) {
-  if (gather == nullptr) {
+  if (gather == nullptr && row_scale == nullptr) {
     clear_error();
-    return fail("grouped_reduce_gather: gather is NULL");
+    return fail("grouped_reduce_gather: neither gather nor a row scale");
   }
-  return grouped_reduce_impl(g, ldg, gather, k, l, ldl, rows, N, R, scaling, offsets, E, out, o_se, o_sn, o_sr, stream);
+  return grouped_reduce_impl(g, ldg, gather, k, row_scale, row_scale_dtype, scale_index, l, ldl, rows, N, R, scaling,
+                             offsets, E, out, o_se, o_sn, o_sr, stream);
 }

@@ -195,7 +195,9 @@ def test_qwen3_moe_sized_projection_stays_within_tolerance():
         assert rel(a, b) < BF16_TOL, (name, rel(a, b))
 
 
-@pytest.mark.parametrize("E,A,B", [(3, 16, 200), (2, 130, 48), (1, 64, 64), (5, 1, 7)])
+@pytest.mark.parametrize("E,A,B", [(3, 16, 200), (2, 130, 48), (1, 64, 64), (5, 1, 7), (4, 300, 16), (3, 32, 300),
+                                   (2, 257, 32), (128, 16, 2048), (2, 12, 40), (3, 2048, 16), (2, 48, 136),
+                                   (2, 32, 1000), (3, 1000, 32), (1, 136, 200)])
 def test_the_batched_transpose_is_exact(E, A, B):
     """mlora_transpose (the adapters' roles in the input-gradient product): exact, any strides."""
     from meepsquared_amd._grouped import _transposed

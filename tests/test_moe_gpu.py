@@ -115,3 +115,48 @@ def test_layer_with_nf4_stacks_on_a_packed_varlen_batch(is_transposed):
     got, want = run_layer(T, 2048, 768, 128, 8, 16, 32, is_transposed, seed=4, nf4=True)
     for name in want:
         assert rel(got[name], want[name]) < 3e-2, (name, rel(got[name], want[name]))
+
+
+@pytest.mark.parametrize("is_transposed", [False, True])
+@pytest.mark.parametrize("weights_dtype", [torch.bfloat16, torch.float32])
+def test_the_combined_down_product_matches_the_product_then_the_combine(is_transposed, weights_dtype):
+    """lora_linear_combined (the down product and the combine in one Function, the backward reading the
+    output gradient through perm) against lora_linear followed by the combine: the same output and
+    weight-gradient bits, the input and adapter gradients within bf16 rounding of each other (the
+    weights enter after different roundings)."""
+    from meepsquared_amd import _grouped, _moe, sort_by_expert, topk_softmax
+
+    torch.manual_seed(11)
+    T, I, H, E, k, r = 300, 128, 192, 8, 2, 16
+    dev = "cuda"
+    logits = torch.randn(T, E, device=dev)
+    w, idx = topk_softmax(logits.to(torch.bfloat16), k, weights_dtype=weights_dtype)
+    idx = torch.where(torch.rand(idx.shape, device=dev) < 0.05, torch.full_like(idx, E), idx)  # a few sentinels
+    perm, inv, offsets = sort_by_expert(idx, E)
+    act = torch.randn(T * k, I, device=dev).bfloat16()
+    down = (torch.randn((E, I, H) if is_transposed else (E, H, I), device=dev) * 0.05).bfloat16()
+    if is_transposed:
+        lhs, rhs = torch.randn(E, I, r, device=dev) * 0.1, torch.randn(E, r, H, device=dev) * 0.1
+    else:
+        lhs, rhs = torch.randn(E, H, r, device=dev) * 0.1, torch.randn(E, r, I, device=dev) * 0.1
+    dres = torch.randn(T, H, device=dev).bfloat16()
+
+    def run(combined):
+        a = act.clone().requires_grad_()
+        ww = w.detach().clone().requires_grad_()
+        l_, r_ = lhs.bfloat16().requires_grad_(), rhs.bfloat16().requires_grad_()
+        if combined:
+            out = _grouped.lora_linear_combined(a, ww, perm, inv, k, down, None, offsets, is_transposed, l_, r_, 2.0)
+        else:
+            y = _grouped.lora_linear(a, down, None, offsets, is_transposed, l_, r_, 2.0)
+            out = _moe._Combine.apply(y, ww, inv, offsets, k)
+        out.backward(dres)
+        return out.detach(), ww.grad, a.grad, l_.grad, r_.grad
+
+    got, want = run(True), run(False)
+    assert torch.equal(got[0], want[0])
+    assert torch.equal(got[1], want[1])
+    valid = int(offsets[-1])  # rows past it are sentinels' and take no gradient
+    assert rel(got[2][:valid], want[2][:valid]) < 1e-2
+    for i in (3, 4):
+        assert rel(got[i], want[i]) < 1e-2
