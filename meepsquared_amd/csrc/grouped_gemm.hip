@@ -607,6 +607,7 @@ static int grouped_gemm_impl(const void* x, int64_t ldx, const int64_t* gather, 
     return fail("grouped_gemm: out needs a 16-byte aligned base and a row stride (%lld) that is a multiple of 8 and >= N",
                 (long long)ldo);
   if ((int64_t)BM * ldx * 2 > 0x7FFFFFF0) return fail("grouped_gemm: row stride %lld too large", (long long)ldx);
+  if ((int64_t)BM * ldo * 2 > 0x7FFFFFF0) return fail("grouped_gemm: out row stride %lld too large", (long long)ldo);
   const bool bkc = w_sk == 1;
   if (!bkc && w_sn != 1)
     return fail("grouped_gemm: the stack needs a unit stride along k or n (w_sk=%lld, w_sn=%lld)", (long long)w_sk,

@@ -350,15 +350,15 @@ __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_ker
   bf16* const slots[STAGES] = {slot0, slot1};
 #endif
   extern __shared__ __attribute__((aligned(16))) int tile_map[];
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int tid0 = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid0 >> 6);
   const int wm = wave / WAVES_N, wn = wave % WAVES_N;
   const int E = p.E;
 
   bf16* Ls = slot0;  // epilogue: [BM][LP] and [BN][LP], in slots the ring has finished with
   bf16* Lb = slot1;
 
-  build_tile_ends(p, tile_map, tid);
+  build_tile_ends(p, tile_map, tid0);
   const int nb = (p.N + BN - 1) / BN;
   const int64_t total = (int64_t)__builtin_amdgcn_readfirstlane(tile_map[E - 1]) * nb;
   const int xcd = blockIdx.x % kXcds, wg_slot = blockIdx.x / kXcds, per_xcd = gridDim.x / kXcds;
@@ -367,6 +367,11 @@ __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_ker
   const int nk = (p.K + BK - 1) / BK;
 
   for (int64_t item = beg + wg_slot; item < end; item += per_xcd) {
+    // the thread index taken afresh for every item: values derived from it are computed where they
+    // are used, not hoisted out of this loop to hold registers through every K loop and epilogue
+    int tid = tid0;
+    asm volatile("" : "+v"(tid));
+    const int lane = tid & 63;
     const Item it = decode(p, item, nb, tile_map);
     const int e = it.e, n0 = it.n0, mrows = it.mrows;
     const int64_t row0 = it.row0;
@@ -414,23 +419,31 @@ __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_ker
     wait_vm<0>();     // the zero-filled copies queued past the end of K
     __syncthreads();  // every wave is done with the ring (all copies waited for in the loop)
 
-    // ---- epilogue: as in grouped_gemm.hip ----
+    // ---- epilogue ----
+    // Everything the stores need is read first: the adapters' tiles, the per-column stack scales and
+    // the bias into LDS, the row scales into registers.  A vector-memory load issued after the first
+    // output store would wait for every store before it (one in-order counter covers both), so the
+    // stores run back to back with nothing but LDS reads between them.
     const int col_l = 4 * (lane >> 5);
-    f32x4 cs[FN][4];
+    float* Lc = (float*)(Lb + BN * LP);  // [BN] per-column stack scale (MLORA_SCALE_ROW)
+    bf16* Lbias = (bf16*)(Lc + BN);      // [BN] bias
+    const bool col_scale = p.scale_kind == MLORA_SCALE_ROW, has_bias = p.bias != nullptr;
+    const float cexp = p.scale_kind == MLORA_SCALE_EXPERT ? p.scale[e] : 1.f;
+    if (tid < BN && (col_scale || has_bias)) {
+      const int n = n0 + tid;
+      if (col_scale) Lc[tid] = n < p.N ? p.scale[(int64_t)e * p.scale_se + n] : 0.f;
+      if (has_bias) Lbias[tid] = n < p.N ? p.bias[(int64_t)e * p.bias_se + n] : (bf16)0.f;
+    }
+    float rs[FM];  // each row's output scale (the combine weight of a gathered gradient row)
 #pragma unroll
-    for (int j = 0; j < FN; ++j)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        if (p.scale_kind == MLORA_SCALE_EXPERT) {
-          const float c = p.scale[e];
-          cs[j][g] = f32x4{c, c, c, c};
-        } else if (p.scale_kind == MLORA_SCALE_ROW) {
-          const int n = n0 + (j * WAVES_N + wn) * 32 + 8 * g + col_l;
-          cs[j][g] = n < p.N ? *(const f32x4*)(p.scale + (int64_t)e * p.scale_se + n) : f32x4{};
-        } else {
-          cs[j][g] = f32x4{1.f, 1.f, 1.f, 1.f};
-        }
+    for (int i = 0; i < FM; ++i) {
+      const int row = (i * WAVES_M + wm) * 32 + (lane & 31);
+      rs[i] = 1.f;
+      if (p.row_scale != nullptr && i < am && row < mrows) {
+        const int64_t si = p.gather[row0 + row];
+        rs[i] = p.row_scale_dt == MLORA_DT_F32 ? ((const float*)p.row_scale)[si] : (float)((const bf16*)p.row_scale)[si];
       }
+    }
     if constexpr (NRB > 0) {
 #pragma unroll
       for (int q = 0; q < kLS; ++q) {
@@ -448,7 +461,10 @@ __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_ker
         const int n = n0 + nn;
         *(u32x4*)(Lb + nn * LP + rc) = ld128(rbt, n < p.N ? (uint32_t)((n * p.bt_sn + rc) * 2) : kOob);
       }
-      __syncthreads();
+    }
+    __syncthreads();
+    wait_vm<0>();  // the row scales (and every other load) are in before the first store
+    if constexpr (NRB > 0) {
       if (p.low != nullptr && it.nblk == 0) {
         for (int c = tid; c < BM * RP / 8; c += kThreads) {
           const int m = c / (RP / 8), rc = (c - m * (RP / 8)) * 8;
@@ -457,16 +473,13 @@ __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_ker
       }
     }
     const bool lora_on = NRB > 0 && p.scaling != 0.f;
+    // the item's rows of out through a buffer resource: 32-bit offsets, stores past its rows dropped
+    const rsrc_t ro = make_rsrc(p.out + row0 * p.ldo, (int64_t)mrows * p.ldo * 2);
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
       const int row = (i * WAVES_M + wm) * 32 + (lane & 31);
       if (i >= am) continue;
-      bf16* orow = p.out + (row0 + row) * p.ldo;
-      float rs = 1.f;  // the row's output scale (the combine weight of a gathered gradient row)
-      if (p.row_scale != nullptr && row < mrows) {
-        const int64_t si = p.gather[row0 + row];
-        rs = p.row_scale_dt == MLORA_DT_F32 ? ((const float*)p.row_scale)[si] : (float)((const bf16*)p.row_scale)[si];
-      }
+      const uint32_t orow = (uint32_t)(row * p.ldo * 2);
 #pragma unroll
       for (int j = 0; j < FN; ++j) {
         if (j >= an) continue;
@@ -481,24 +494,41 @@ __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_ker
             }
           }
         }
-        if (row >= mrows) continue;
+        // lane l holds columns 8g + 4(l/32) .. +3 of its row for g = 0..3; one swap of the lanes'
+        // halves per pair of groups gives lane l < 32 columns 16h .. 16h+7 and lane l + 32 columns
+        // 16h+8 .. 16h+15 (h = 0, 1): 16-byte stores, each row's 32 columns in two instructions
+        u32x2 pk[4];
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-          const int n = n0 + (j * WAVES_N + wn) * 32 + 8 * g + col_l;
-          if (n >= p.N) continue;
-          f32x4 bias = {0.f, 0.f, 0.f, 0.f};
-          if (p.bias != nullptr) {
-            const bf16* bp = p.bias + (int64_t)e * p.bias_se + n;
-            bias = f32x4{(float)bp[0], (float)bp[1], (float)bp[2], (float)bp[3]};
+          const int nn = (j * WAVES_N + wn) * 32 + 8 * g + col_l;  // column within the tile
+          f32x4 c = {cexp, cexp, cexp, cexp}, bias = {0.f, 0.f, 0.f, 0.f};
+          if (col_scale) c = *(const f32x4*)(Lc + nn);
+          if (has_bias) {
+            const u32x2 b2 = *(const u32x2*)(Lbias + nn);
+            bias = f32x4{bf16_bits_to_f32(b2[0] & 0xFFFFu), bf16_bits_to_f32(b2[0] >> 16), bf16_bits_to_f32(b2[1] & 0xFFFFu),
+                         bf16_bits_to_f32(b2[1] >> 16)};
           }
           float o[4];
 #pragma unroll
           for (int q = 0; q < 4; ++q)
-            o[q] = (acc[i][j][4 * g + q] * cs[j][g][q] + p.scaling * t[4 * g + q]) * rs + bias[q];
-          u32x2 v;
-          v[0] = pack_bf16x2(o[0], o[1]);
-          v[1] = pack_bf16x2(o[2], o[3]);
-          *(u32x2*)(orow + n) = v;
+            o[q] = (acc[i][j][4 * g + q] * c[q] + p.scaling * t[4 * g + q]) * rs[i] + bias[q];
+          pk[g] = u32x2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
+        }
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int d = 0; d < 2; ++d) {
+            const auto sw = __builtin_amdgcn_permlane32_swap(pk[2 * h][d], pk[2 * h + 1][d], false, false);
+            pk[2 * h][d] = sw[0];
+            pk[2 * h + 1][d] = sw[1];
+          }
+        if (row >= mrows) continue;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int n = n0 + (j * WAVES_N + wn) * 32 + 16 * h + 8 * (lane >> 5);
+          if (n < p.N)
+            __builtin_amdgcn_raw_buffer_store_b128(u32x4{pk[2 * h][0], pk[2 * h][1], pk[2 * h + 1][0], pk[2 * h + 1][1]},
+                                                   ro, orow + (uint32_t)(n - n0) * 2 + (uint32_t)n0 * 2, 0, 0);
         }
       }
     }
@@ -506,8 +536,8 @@ __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_ker
 }
 
 static size_t lds_bytes(int E) { return (size_t)E * sizeof(int); }
-static_assert(BM * (kMaxRank + 8) <= SlotSize<4>::kElems && BN * (kMaxRank + 8) <= SlotSize<4>::kElems,
-              "the epilogue's low and B^T tiles must fit in the slots they reuse");
+static_assert(BM * (kMaxRank + 8) <= SlotSize<4>::kElems && BN * (kMaxRank + 8) + BN * 3 <= SlotSize<4>::kElems,
+              "the epilogue's low, B^T, column-scale and bias tiles must fit in the slots they reuse");
 static_assert(STAGES * SlotSize<4>::kElems * 2 + 4096 * 4 <= 163840, "the slots and the largest tile map fit in LDS");
 
 template <bool BKC, int NRB>
