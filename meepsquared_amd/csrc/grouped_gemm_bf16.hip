@@ -425,7 +425,8 @@ __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_ker
     // output store would wait for every store before it (one in-order counter covers both), so the
     // stores run back to back with nothing but LDS reads between them.
     const int col_l = 4 * (lane >> 5);
-    float* Lc = (float*)(Lb + BN * LP);  // [BN] per-column stack scale (MLORA_SCALE_ROW)
+    // [BN] per-column stack scale (MLORA_SCALE_ROW) and [BN] bias: after B^T, or in the third slot
+    float* Lc = (float*)(STAGES == 4 ? slots[STAGES - 2] : Lb + BN * LP);
     bf16* Lbias = (bf16*)(Lc + BN);      // [BN] bias
     const bool col_scale = p.scale_kind == MLORA_SCALE_ROW, has_bias = p.bias != nullptr;
     const float cexp = p.scale_kind == MLORA_SCALE_EXPERT ? p.scale[e] : 1.f;
@@ -473,6 +474,7 @@ __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_ker
       }
     }
     const bool lora_on = NRB > 0 && p.scaling != 0.f;
+    const bool plain = !col_scale && cexp == 1.f && p.row_scale == nullptr && !has_bias;
     // the item's rows of out through a buffer resource: 32-bit offsets, stores past its rows dropped
     const rsrc_t ro = make_rsrc(p.out + row0 * p.ldo, (int64_t)mrows * p.ldo * 2);
 #pragma unroll
@@ -498,21 +500,31 @@ __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_ker
         // halves per pair of groups gives lane l < 32 columns 16h .. 16h+7 and lane l + 32 columns
         // 16h+8 .. 16h+15 (h = 0, 1): 16-byte stores, each row's 32 columns in two instructions
         u32x2 pk[4];
+        if (plain) {  // no stack scale, row scale or bias: one fma per value
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int nn = (j * WAVES_N + wn) * 32 + 8 * g + col_l;  // column within the tile
-          f32x4 c = {cexp, cexp, cexp, cexp}, bias = {0.f, 0.f, 0.f, 0.f};
-          if (col_scale) c = *(const f32x4*)(Lc + nn);
-          if (has_bias) {
-            const u32x2 b2 = *(const u32x2*)(Lbias + nn);
-            bias = f32x4{bf16_bits_to_f32(b2[0] & 0xFFFFu), bf16_bits_to_f32(b2[0] >> 16), bf16_bits_to_f32(b2[1] & 0xFFFFu),
-                         bf16_bits_to_f32(b2[1] >> 16)};
+          for (int g = 0; g < 4; ++g) {
+            float o[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) o[q] = __builtin_fmaf(p.scaling, t[4 * g + q], acc[i][j][4 * g + q]);
+            pk[g] = u32x2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
           }
-          float o[4];
+        } else {
 #pragma unroll
-          for (int q = 0; q < 4; ++q)
-            o[q] = (acc[i][j][4 * g + q] * c[q] + p.scaling * t[4 * g + q]) * rs[i] + bias[q];
-          pk[g] = u32x2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
+          for (int g = 0; g < 4; ++g) {
+            const int nn = (j * WAVES_N + wn) * 32 + 8 * g + col_l;  // column within the tile
+            f32x4 c = {cexp, cexp, cexp, cexp}, bias = {0.f, 0.f, 0.f, 0.f};
+            if (col_scale) c = *(const f32x4*)(Lc + nn);
+            if (has_bias) {
+              const u32x2 b2 = *(const u32x2*)(Lbias + nn);
+              bias = f32x4{bf16_bits_to_f32(b2[0] & 0xFFFFu), bf16_bits_to_f32(b2[0] >> 16),
+                           bf16_bits_to_f32(b2[1] & 0xFFFFu), bf16_bits_to_f32(b2[1] >> 16)};
+            }
+            float o[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+              o[q] = (acc[i][j][4 * g + q] * c[q] + p.scaling * t[4 * g + q]) * rs[i] + bias[q];
+            pk[g] = u32x2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
+          }
         }
 #pragma unroll
         for (int h = 0; h < 2; ++h)
@@ -536,7 +548,8 @@ __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_ker
 }
 
 static size_t lds_bytes(int E) { return (size_t)E * sizeof(int); }
-static_assert(BM * (kMaxRank + 8) <= SlotSize<4>::kElems && BN * (kMaxRank + 8) + BN * 3 <= SlotSize<4>::kElems,
+static_assert(BM * (kMaxRank + 8) <= SlotSize<4>::kElems &&
+                  BN * (kMaxRank + 8) + (STAGES == 4 ? 0 : BN * 3) <= SlotSize<4>::kElems,
               "the epilogue's low, B^T, column-scale and bias tiles must fit in the slots they reuse");
 static_assert(STAGES * SlotSize<4>::kElems * 2 + 4096 * 4 <= 163840, "the slots and the largest tile map fit in LDS");
 
