@@ -153,6 +153,10 @@ def read_traffic():
 
 def roofline(c, achieved, config):
     """The grouped product's achieved rate against the MFMA peak it runs on (traffic measured for config 1)."""
+    if c.get("stack") == "fp8" and os.environ.get("MEEPSQUARED_FP8_PRODUCTS") == "0":
+        return {"bound": "mfma", "kernel": "grouped_gemm_bf16_kernel / register-staged kernel, fp8 stacks decoded to bf16",
+                "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None}
     if c.get("stack") == "fp8":
         return {"bound": "mfma", "kernel": "fp8_prep + fp8_gemm_kernel (4 products per step, timed together)",
                 "achieved": round(achieved, 2), "peak": PEAK_FP8_TFLOPS, "unit": "TFLOP/s",
@@ -192,6 +196,9 @@ def main():
                     help="1: the bf16 Qwen3-shaped layer (default, the headline); 2: Mixtral-shaped with Zipf-loaded "
                          "experts; 3: config 1 with fp8 e4m3 stacks (per-row scales) on the fp8 MFMA; 4: config 1 "
                          "shapes on a packed varlen batch with NF4 stacks")
+    ap.add_argument("--bf16-products", action="store_true",
+                    help="config 3 with the products in bf16 (the fp8 stack decoded in registers, the reference's "
+                         "default for fp8 stacks) instead of on the fp8 MFMA")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {a.gpus})", file=sys.stderr)
@@ -217,7 +224,9 @@ def main():
         down8, down_s = _fp8.quantize_stack(down, per_row=True)
         del gate_up, down
         experts = Experts(gate_up8, down8, gate_up_proj_scale_inv=gate_up_s, down_proj_scale_inv=down_s)
-        os.environ["MEEPSQUARED_FP8_PRODUCTS"] = "1"
+        os.environ["MEEPSQUARED_FP8_PRODUCTS"] = "0" if a.bf16_products else "1"
+        if a.bf16_products:
+            c = dict(c, name=c["name"] + ", bf16 products (fp8 stacks decoded in registers)")
     elif c.get("stack") == "nf4":
         from meepsquared_amd import _nf4
 
@@ -290,7 +299,8 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": {"fp8": "fp8-e4m3 products (bf16 activations, per-row fp32 stack scales)",
+        "dtype": {"fp8": "bf16 products (fp8-e4m3 stacks decoded in registers, per-row fp32 scales)" if a.bf16_products
+                  else "fp8-e4m3 products (bf16 activations, per-row fp32 stack scales)",
                   "nf4": "bf16 products (NF4 stacks decoded in registers)"}.get(c.get("stack"), "bf16"),
         "data": "synthetic (seeded N(0,1) x and logits, N(0,0.02) W, Kaiming-uniform A, N(0,0.01) B)",
         "config": {"workload": c["name"], "tokens": T, "hidden": H, "moe_intermediate": I, "experts": E,

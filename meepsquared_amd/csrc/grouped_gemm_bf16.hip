@@ -149,19 +149,36 @@ __device__ __forceinline__ Item decode(const GemmArgs& p, int64_t item, int nb, 
 // copies still landing in the others and does not wait for those.
 // The A^T tile is copied with RD rows: the rank padded so that the copies split over the eight
 // waves in whole runs of lanes (rank 48 is copied as 64 rows, the last 16 read as zeros).
-template <int NRB>
+// The stack's element type in LDS: bf16, or fp8 e4m3 / NF4 copied as stored (k contiguous) and
+// decoded to bf16 in registers as each MFMA operand is read.
+enum : int { kWBf16 = 0, kWFp8 = 1, kWNf4 = 2 };
+template <int WT>
+struct WTile {
+  static constexpr int RowBytes = WT == kWBf16 ? BK * 2 : WT == kWFp8 ? BK : BK / 2;  // one row of the stage
+  static constexpr int Chunks = RowBytes / 16;                                         // 16-byte chunks per row
+  static constexpr int Elems = BN * RowBytes / 2;                                      // bf16 slots of LDS
+  static constexpr int WI = BN * Chunks / (64 * NW);                                   // copies per wave
+  static_assert(BN * Chunks % (64 * NW) == 0, "the stack tile splits evenly over the waves");
+};
+// [n][k] byte tiles of fp8 (4 chunks per row) and NF4 (2): chunk c of row n in slot c ^ g(n)
+template <int WT>
+__device__ __forceinline__ int swz_q(int n) { return WT == kWFp8 ? (n >> 2) & 3 : (n >> 3) & 1; }
+
+template <int NRB, int WT = kWBf16>
 struct SlotSize {
   static constexpr int RD = (NRB == 3 ? 4 : NRB) * 16;
-  static constexpr int kElems = (BM + BN + RD) * BK;
+  static constexpr int kElems = BM * BK + WTile<WT>::Elems + RD * BK;
 };
 
 // Per-lane DMA addressing of one item, fixed for its whole K loop: byte offsets at k = 0 and the
 // k of each lane's chunk (a huge k marks a column past N: never in range).
-template <bool BKC, int NRB>
+template <bool BKC, int NRB, int WT>
 struct Feed {
+  static_assert(WT == kWBf16 || BKC, "fp8 and NF4 stacks are read with k contiguous");
   static constexpr int RP = NRB * 16;
-  static constexpr int CPW = SlotSize<NRB>::RD * BK / 8 / NW;  // A^T chunks per wave per stage
+  static constexpr int CPW = SlotSize<NRB, WT>::RD * BK / 8 / NW;  // A^T chunks per wave per stage
   static_assert(NRB == 0 || (CPW > 0 && 64 % CPW == 0), "each wave's A^T chunks lie in one 64-lane copy");
+  static constexpr int WI = WTile<WT>::WI;
   // this wave's copies per stage: XI of x, WI of the stack, one (lane-masked) of A^T
   static constexpr int PS = XI + WI + (NRB > 0 ? 1 : 0);
   rsrc_t rx, rw, ra;
@@ -188,7 +205,14 @@ struct Feed {
 #pragma unroll
     for (int q = 0; q < WI; ++q) {
       const int instr = wave * WI + q, ci = instr * 64 + lane;
-      if constexpr (BKC) {  // [n][k]
+      if constexpr (WT != kWBf16) {  // [n][k] bytes: fp8 one per k, NF4 one per two k
+        constexpr int CH = WTile<WT>::Chunks;
+        const int row = ci / CH, c = (ci % CH) ^ swz_q<WT>(row);
+        const int n = n0 + row;
+        const int64_t rowb = WT == kWFp8 ? (int64_t)n * p.w_sn : (int64_t)n * p.w_sn / 2;
+        wo[q] = n < p.N ? (uint32_t)(rowb + c * 16) : 0u;
+        wk[q] = n < p.N ? c * (WT == kWFp8 ? 16 : 32) : (1 << 30);
+      } else if constexpr (BKC) {  // [n][k]
         const int row = ci / CPR, c = (ci % CPR) ^ swz_f(row);
         const int n = n0 + row;
         wo[q] = n < p.N ? (uint32_t)(((int64_t)n * p.w_sn + c * 8) * 2) : 0u;
@@ -201,7 +225,7 @@ struct Feed {
       }
       wd[q] = BM * BK + instr * 512;
     }
-    wstep = BKC ? 2 : 2 * p.w_sk;
+    wstep = WT == kWFp8 ? 1 : BKC ? 2 : 2 * p.w_sk;
     if constexpr (NRB > 0) {
       // wave w copies chunks [w * CPW, (w + 1) * CPW) of the A^T tile: lanes of one 64-chunk
       // instruction block, the others masked off (their LDS bytes belong to other waves)
@@ -210,7 +234,7 @@ struct Feed {
       const int r = ci / CPR, c = (ci % CPR) ^ swz_f(r);
       ao = (uint32_t)((r * p.at_sr + c * 8) * 2);
       ak = c * 8;
-      ad = (BM + BN) * BK + blk * 512;
+      ad = BM * BK + WTile<WT>::Elems + blk * 512;
       a_on = lane >= (c0 & 63) && lane < (c0 & 63) + CPW;
     }
   }
@@ -224,7 +248,7 @@ struct Feed {
       dma16(rx, slot + xd[q], xk[q] + k0 < p.K ? xo[q] + (uint32_t)(k0 * 2) : kOob);
 #pragma unroll
     for (int q = 0; q < WI; ++q)
-      dma16(rw, slot + wd[q], wk[q] + k0 < p.K ? wo[q] + (uint32_t)(k0 * wstep) : kOob);
+      dma16(rw, slot + wd[q], wk[q] + k0 < p.K ? wo[q] + (WT == kWNf4 ? (uint32_t)(k0 / 2) : (uint32_t)(k0 * wstep)) : kOob);
     if constexpr (NRB > 0) {
       if (a_on) dma16(ra, slot + ad, ak + k0 < p.K ? ao + (uint32_t)(k0 * 2) : kOob);
     }
@@ -232,9 +256,19 @@ struct Feed {
 };
 
 // the stack's fragment for MFMA (32 columns n at nb, 8 consecutive k at kb + 8*(lane/32))
-template <bool BKC>
+template <bool BKC, int WT = kWBf16>
 __device__ __forceinline__ bf16x8 w_frag(const bf16* bs, int nb, int kk, int lane) {
-  if constexpr (BKC) {
+  if constexpr (WT == kWFp8) {
+    // eight e4m3 bytes of row n (16-byte chunk kk, half lane/32), converted exactly to bf16
+    const int n = nb + (lane & 31);
+    const u32x2 v = *(const u32x2*)((const uint8_t*)bs + n * BK + ((kk ^ swz_q<WT>(n)) << 4) + 8 * (lane >> 5));
+    typedef unsigned u32x4_ __attribute__((ext_vector_type(4)));
+    const u32x4_ w = {__builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(v[0], 1.f, false)),
+                      __builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(v[0], 1.f, true)),
+                      __builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(v[1], 1.f, false)),
+                      __builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(v[1], 1.f, true))};
+    return __builtin_bit_cast(bf16x8, w);
+  } else if constexpr (BKC) {
     return *(const bf16x8*)(bs + swz_rk(nb + (lane & 31), kk * 2 + (lane >> 5)));
   } else {
     // ds_read_b64_tr_b16: in each group of 16 lanes, source lane s points at (k0 + s/4, n0 + 4*(s%4))
@@ -253,12 +287,88 @@ __device__ __forceinline__ bf16x8 w_frag(const bf16* bs, int nb, int kk, int lan
   }
 }
 
+// ---- NF4 ----
+// A stage is one 64-k block of every stack row, so a lane needs one absmax per column block per
+// stage: absmax = code2[q] · absmax2 + offset (rounded after the product and after the sum, as the
+// standalone dequantiser), with q and absmax2 loaded a stage ahead.  From it the lane builds its
+// table of the sixteen decoded values bf16(code[c] · absmax), kept as a low-byte and a high-byte
+// plane (four dwords each), and decodes eight nibbles with byte permutes: four values per lookup.
+struct Nf4Pipe {
+  int64_t blk[FN];  // the block index of this lane's column j at k = 0, or -1 past N
+  uint32_t q[FN];
+  float a2[FN];
+  __device__ __forceinline__ void init(const GemmArgs& p, int e, int n0, int wn, int lane) {
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const int n = n0 + (j * WAVES_N + wn) * 32 + (lane & 31);
+      blk[j] = n < p.N ? ((int64_t)e * p.w_se + (int64_t)n * p.w_sn) >> 6 : -1;
+    }
+  }
+  __device__ __forceinline__ void load(const GemmArgs& p, int kt) {
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const bool ok = blk[j] >= 0 && kt * BK < p.K;
+      const int64_t b = blk[j] + kt;
+      q[j] = ok ? p.nf4_q[b] : 0u;
+      a2[j] = ok ? p.nf4_absmax2[b >> 8] : 0.f;
+    }
+  }
+};
+
+__device__ __forceinline__ float nf4_absmax(float c2, float a2, float off) {
+#pragma clang fp contract(off)
+  return c2 * a2 + off;
+}
+
+// the decoded values of one block: lo[m] / hi[m] hold the low / high bytes of entries 4m .. 4m+3
+__device__ __forceinline__ void nf4_table(const float* code, float absmax, uint32_t (&lo)[4], uint32_t (&hi)[4]) {
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const f32x4 c = *(const f32x4*)(code + 4 * m);
+    const uint32_t p0 = pack_bf16x2(c[0] * absmax, c[1] * absmax), p1 = pack_bf16x2(c[2] * absmax, c[3] * absmax);
+    lo[m] = __builtin_amdgcn_perm(p1, p0, 0x06040200u);
+    hi[m] = __builtin_amdgcn_perm(p1, p0, 0x07050301u);
+  }
+}
+
+// four byte-sized indices (0..15) -> their entries' low and high bytes
+__device__ __forceinline__ void nf4_look(uint32_t g, const uint32_t (&lo)[4], const uint32_t (&hi)[4], uint32_t& lb,
+                                         uint32_t& hb) {
+  const uint32_t sel = g & 0x07070707u;
+  // 0xFF in the bytes whose index is 8 or more (permute selector 13), 0x00 elsewhere (selector 12)
+  const uint32_t m = __builtin_amdgcn_perm(0u, 0u, ((g >> 3) & 0x01010101u) | 0x0C0C0C0Cu);
+  lb = __builtin_amdgcn_perm(lo[1], lo[0], sel);
+  hb = __builtin_amdgcn_perm(hi[1], hi[0], sel);
+  lb = (__builtin_amdgcn_perm(lo[3], lo[2], sel) & m) | (lb & ~m);
+  hb = (__builtin_amdgcn_perm(hi[3], hi[2], sel) & m) | (hb & ~m);
+}
+
+// eight NF4 codes (byte j: element 2j in the high nibble, 2j+1 in the low) -> eight bf16
+__device__ __forceinline__ bf16x8 nf4_decode(uint32_t x, const uint32_t (&lo)[4], const uint32_t (&hi)[4]) {
+  uint32_t el, eh, ol, oh;
+  nf4_look((x >> 4) & 0x0F0F0F0Fu, lo, hi, el, eh);  // elements 0, 2, 4, 6
+  nf4_look(x & 0x0F0F0F0Fu, lo, hi, ol, oh);         // elements 1, 3, 5, 7
+  const uint32_t e02 = __builtin_amdgcn_perm(eh, el, 0x05010400u), e46 = __builtin_amdgcn_perm(eh, el, 0x07030602u);
+  const uint32_t o13 = __builtin_amdgcn_perm(oh, ol, 0x05010400u), o57 = __builtin_amdgcn_perm(oh, ol, 0x07030602u);
+  typedef unsigned u32x4_ __attribute__((ext_vector_type(4)));
+  const u32x4_ w = {__builtin_amdgcn_perm(o13, e02, 0x05040100u), __builtin_amdgcn_perm(o13, e02, 0x07060302u),
+                    __builtin_amdgcn_perm(o57, e46, 0x05040100u), __builtin_amdgcn_perm(o57, e46, 0x07060302u)};
+  return __builtin_bit_cast(bf16x8, w);
+}
+
 // The MFMAs of one stage held in `slot` for a wave with AM live row blocks.
-template <int AM, bool BKC, int NRB>
-__device__ __forceinline__ void compute(const bf16* slot, int lane, int wm, int wn, f32x16 (&acc)[FM][FN],
-                                        f32x4 (&lacc)[kLS][NRB > 0 ? NRB : 1]) {
+template <int AM, bool BKC, int NRB, int WT>
+__device__ __forceinline__ void compute(const GemmArgs& p, const bf16* slot, int lane, int wm, int wn,
+                                        f32x16 (&acc)[FM][FN], f32x4 (&lacc)[kLS][NRB > 0 ? NRB : 1],
+                                        Nf4Pipe& nf, const float* code, float off, int kt) {
   const bf16* as = slot;
   const bf16* bs = slot + BM * BK;
+  uint32_t tlo[WT == kWNf4 ? FN : 1][4], thi[WT == kWNf4 ? FN : 1][4];
+  if constexpr (WT == kWNf4) {  // this stage's tables, then the next stage's block scales
+#pragma unroll
+    for (int j = 0; j < FN; ++j) nf4_table(code, nf4_absmax(code[16 + nf.q[j]], nf.a2[j], off), tlo[j], thi[j]);
+    nf.load(p, kt + 1);
+  }
   if constexpr (AM > 0) {
 #pragma unroll
     for (int kk = 0; kk < BK / 16; ++kk) {
@@ -267,7 +377,17 @@ __device__ __forceinline__ void compute(const bf16* slot, int lane, int wm, int 
       for (int i = 0; i < AM; ++i)
         af[i] = *(const bf16x8*)(as + swz_rk((i * WAVES_M + wm) * 32 + (lane & 31), kk * 2 + (lane >> 5)));
 #pragma unroll
-      for (int j = 0; j < FN; ++j) bfr[j] = w_frag<BKC>(bs, (j * WAVES_N + wn) * 32, kk, lane);
+      for (int j = 0; j < FN; ++j) {
+        if constexpr (WT == kWNf4) {
+          // eight codes: byte 8kk/2 + 4(lane/32) of row n (16-byte chunk kk/2)
+          const int n = (j * WAVES_N + wn) * 32 + (lane & 31);
+          const uint32_t x = *(const uint32_t*)((const uint8_t*)bs + n * (BK / 2) +
+                                                (((kk >> 1) ^ swz_q<WT>(n)) << 4) + (kk & 1) * 8 + 4 * (lane >> 5));
+          bfr[j] = nf4_decode(x, tlo[j], thi[j]);
+        } else {
+          bfr[j] = w_frag<BKC, WT>(bs, (j * WAVES_N + wn) * 32, kk, lane);
+        }
+      }
 #pragma unroll
       for (int i = 0; i < AM; ++i)
 #pragma unroll
@@ -275,7 +395,7 @@ __device__ __forceinline__ void compute(const bf16* slot, int lane, int wm, int 
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[j], af[i], acc[i][j], 0, 0, 0);
     }
     if constexpr (NRB > 0) {
-      const bf16* aa = slot + (BM + BN) * BK;
+      const bf16* aa = slot + BM * BK + WTile<WT>::Elems;
 #pragma unroll
       for (int ls = 0; ls < BK / 32; ++ls) {
         bf16x8 ar[NRB];
@@ -299,47 +419,51 @@ __device__ __forceinline__ void compute(const bf16* slot, int lane, int wm, int 
 
 // One iteration of the K loop: wait for this wave's copies of stage kt (slot S), publish every
 // wave's with a barrier, queue stage kt + STAGES - 1 into the slot read one iteration ago, multiply.
-template <int S, int AM, bool BKC, int NRB>
-__device__ __forceinline__ void stage(const GemmArgs& p, const Feed<BKC, NRB>& f, bf16* const (&slots)[STAGES], int kt,
+template <int S, int AM, bool BKC, int NRB, int WT>
+__device__ __forceinline__ void stage(const GemmArgs& p, const Feed<BKC, NRB, WT>& f, bf16* const (&slots)[STAGES], int kt,
                                       int lane, int wm, int wn, f32x16 (&acc)[FM][FN],
-                                      f32x4 (&lacc)[kLS][NRB > 0 ? NRB : 1]) {
-  wait_vm<Feed<BKC, NRB>::PS * (STAGES - 2)>();  // stages kt+1, kt+2 may stay in flight
+                                      f32x4 (&lacc)[kLS][NRB > 0 ? NRB : 1], Nf4Pipe& nf, const float* code,
+                                      float off) {
+  wait_vm<Feed<BKC, NRB, WT>::PS * (STAGES - 2)>();  // stages kt+1, kt+2 may stay in flight
   stage_barrier();
   f.issue(p, slots[(S + STAGES - 1) % STAGES], kt + STAGES - 1);
-  compute<AM, BKC, NRB>(slots[S], lane, wm, wn, acc, lacc);
+  compute<AM, BKC, NRB, WT>(p, slots[S], lane, wm, wn, acc, lacc, nf, code, off, kt);
 }
 
 // The K loop of one item, unrolled by the ring depth so every slot index is a constant.
-template <int AM, bool BKC, int NRB>
-__device__ __forceinline__ void kloop(const GemmArgs& p, const Feed<BKC, NRB>& f, bf16* const (&slots)[STAGES], int nk,
+template <int AM, bool BKC, int NRB, int WT>
+__device__ __forceinline__ void kloop(const GemmArgs& p, const Feed<BKC, NRB, WT>& f, bf16* const (&slots)[STAGES], int nk,
                                       int lane, int wm, int wn, f32x16 (&acc)[FM][FN],
-                                      f32x4 (&lacc)[kLS][NRB > 0 ? NRB : 1]) {
+                                      f32x4 (&lacc)[kLS][NRB > 0 ? NRB : 1], Nf4Pipe& nf, const float* code,
+                                      float off) {
   int kt = 0;
   if constexpr (STAGES == 4) {
     for (; kt + STAGES <= nk; kt += STAGES) {
-      stage<0, AM, BKC, NRB>(p, f, slots, kt, lane, wm, wn, acc, lacc);
-      stage<1, AM, BKC, NRB>(p, f, slots, kt + 1, lane, wm, wn, acc, lacc);
-      stage<2, AM, BKC, NRB>(p, f, slots, kt + 2, lane, wm, wn, acc, lacc);
-      stage<3, AM, BKC, NRB>(p, f, slots, kt + 3, lane, wm, wn, acc, lacc);
+      stage<0, AM, BKC, NRB, WT>(p, f, slots, kt, lane, wm, wn, acc, lacc, nf, code, off);
+      stage<1, AM, BKC, NRB, WT>(p, f, slots, kt + 1, lane, wm, wn, acc, lacc, nf, code, off);
+      stage<2, AM, BKC, NRB, WT>(p, f, slots, kt + 2, lane, wm, wn, acc, lacc, nf, code, off);
+      stage<3, AM, BKC, NRB, WT>(p, f, slots, kt + 3, lane, wm, wn, acc, lacc, nf, code, off);
     }
     const int rem = nk - kt;  // 0 .. 3 stages left
-    if (rem > 0) stage<0, AM, BKC, NRB>(p, f, slots, kt, lane, wm, wn, acc, lacc);
-    if (rem > 1) stage<1, AM, BKC, NRB>(p, f, slots, kt + 1, lane, wm, wn, acc, lacc);
-    if (rem > 2) stage<2, AM, BKC, NRB>(p, f, slots, kt + 2, lane, wm, wn, acc, lacc);
+    if (rem > 0) stage<0, AM, BKC, NRB, WT>(p, f, slots, kt, lane, wm, wn, acc, lacc, nf, code, off);
+    if (rem > 1) stage<1, AM, BKC, NRB, WT>(p, f, slots, kt + 1, lane, wm, wn, acc, lacc, nf, code, off);
+    if (rem > 2) stage<2, AM, BKC, NRB, WT>(p, f, slots, kt + 2, lane, wm, wn, acc, lacc, nf, code, off);
   } else {
     for (; kt + 2 <= nk; kt += 2) {
-      stage<0, AM, BKC, NRB>(p, f, slots, kt, lane, wm, wn, acc, lacc);
-      stage<1, AM, BKC, NRB>(p, f, slots, kt + 1, lane, wm, wn, acc, lacc);
+      stage<0, AM, BKC, NRB, WT>(p, f, slots, kt, lane, wm, wn, acc, lacc, nf, code, off);
+      stage<1, AM, BKC, NRB, WT>(p, f, slots, kt + 1, lane, wm, wn, acc, lacc, nf, code, off);
     }
-    if (kt < nk) stage<0, AM, BKC, NRB>(p, f, slots, kt, lane, wm, wn, acc, lacc);
+    if (kt < nk) stage<0, AM, BKC, NRB, WT>(p, f, slots, kt, lane, wm, wn, acc, lacc, nf, code, off);
   }
 }
 
-template <bool BKC, int NRB>
+template <bool BKC, int NRB, int WT>
 __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_kernel(GemmArgs p) {
   constexpr int RP = NRB * 16;
   constexpr int LP = RP + 8;
-  constexpr int SE = SlotSize<NRB>::kElems;
+  constexpr int SE = SlotSize<NRB, WT>::kElems;
+  static_assert(BM * LP <= SE && BN * LP + (STAGES == 4 ? 0 : BN * 3) <= SE,
+                "the epilogue's low, B^T, column-scale and bias tiles fit in the slots they reuse");
   __shared__ __attribute__((aligned(16))) bf16 slot0[SE];
   __shared__ __attribute__((aligned(16))) bf16 slot1[SE];
 #if MLORA_DMA_STAGES == 4
@@ -358,6 +482,13 @@ __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_ker
   bf16* Ls = slot0;  // epilogue: [BM][LP] and [BN][LP], in slots the ring has finished with
   bf16* Lb = slot1;
 
+  // NF4: the code book (16) and the absmax code book (256) after the tile map
+  float* code = (float*)(tile_map + ((E + 3) & ~3));
+  float off = 0.f;
+  if constexpr (WT == kWNf4) {
+    for (int c = tid0; c < 16 + 256; c += kThreads) code[c] = c < 16 ? p.nf4_code[c] : p.nf4_code2[c - 16];
+    off = p.nf4_offset[0];
+  }
   build_tile_ends(p, tile_map, tid0);
   const int nb = (p.N + BN - 1) / BN;
   const int64_t total = (int64_t)__builtin_amdgcn_readfirstlane(tile_map[E - 1]) * nb;
@@ -380,10 +511,13 @@ __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_ker
     const int am = min(FM, max(0, (mb - wm + WAVES_M - 1) / WAVES_M));
     const int an = min(FN, max(0, (nbk - wn + WAVES_N - 1) / WAVES_N));
 
-    Feed<BKC, NRB> f;
+    Feed<BKC, NRB, WT> f;
     f.rx = p.gather == nullptr ? make_rsrc(p.x + row0 * p.ldx, (int64_t)mrows * p.ldx * 2)
                                : make_rsrc(p.x, p.xrows * p.ldx * 2);
-    f.rw = make_rsrc(p.w + (int64_t)e * p.w_se * 2, p.w_se * 2);
+    {
+      const int64_t ebytes = WT == kWBf16 ? p.w_se * 2 : WT == kWFp8 ? p.w_se : p.w_se / 2;  // one expert's stack
+      f.rw = make_rsrc(p.w + (int64_t)e * ebytes, ebytes);
+    }
     f.ra = f.rx;
     if constexpr (NRB > 0) f.ra = make_rsrc(p.at + (int64_t)e * p.at_se, (int64_t)RP * p.at_sr * 2);
     f.init(p, n0, row0, mrows, wave, lane);
@@ -399,22 +533,27 @@ __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_ker
 #pragma unroll
       for (int j = 0; j < (NRB > 0 ? NRB : 1); ++j) lacc[q][j] = f32x4{};
 
+    Nf4Pipe nf;
+    if constexpr (WT == kWNf4) {
+      nf.init(p, e, n0, wn, lane);
+      nf.load(p, 0);
+    }
     __syncthreads();  // the previous item's epilogue is done with the LDS
 #pragma unroll
     for (int s = 0; s < STAGES - 1; ++s) f.issue(p, slots[s], s);
 
     switch (am) {
-      case FM: kloop<FM, BKC, NRB>(p, f, slots, nk, lane, wm, wn, acc, lacc); break;
+      case FM: kloop<FM, BKC, NRB, WT>(p, f, slots, nk, lane, wm, wn, acc, lacc, nf, code, off); break;
 #if (256 / MLORA_DMA_WM / 32) >= 4
-      case 3: kloop<3, BKC, NRB>(p, f, slots, nk, lane, wm, wn, acc, lacc); break;
+      case 3: kloop<3, BKC, NRB, WT>(p, f, slots, nk, lane, wm, wn, acc, lacc, nf, code, off); break;
 #endif
 #if (256 / MLORA_DMA_WM / 32) >= 3
-      case 2: kloop<2, BKC, NRB>(p, f, slots, nk, lane, wm, wn, acc, lacc); break;
+      case 2: kloop<2, BKC, NRB, WT>(p, f, slots, nk, lane, wm, wn, acc, lacc, nf, code, off); break;
 #endif
 #if (256 / MLORA_DMA_WM / 32) >= 2
-      case 1: kloop<1, BKC, NRB>(p, f, slots, nk, lane, wm, wn, acc, lacc); break;
+      case 1: kloop<1, BKC, NRB, WT>(p, f, slots, nk, lane, wm, wn, acc, lacc, nf, code, off); break;
 #endif
-      default: kloop<0, BKC, NRB>(p, f, slots, nk, lane, wm, wn, acc, lacc); break;
+      default: kloop<0, BKC, NRB, WT>(p, f, slots, nk, lane, wm, wn, acc, lacc, nf, code, off); break;
     }
     wait_vm<0>();     // the zero-filled copies queued past the end of K
     __syncthreads();  // every wave is done with the ring (all copies waited for in the loop)
@@ -547,16 +686,18 @@ __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_ker
   }
 }
 
-static size_t lds_bytes(int E) { return (size_t)E * sizeof(int); }
+static size_t lds_bytes(int E, int WT) { return (size_t)((E + 3) & ~3) * sizeof(int) + (WT == kWNf4 ? 272 * 4 : 0); }
 static_assert(BM * (kMaxRank + 8) <= SlotSize<4>::kElems &&
                   BN * (kMaxRank + 8) + (STAGES == 4 ? 0 : BN * 3) <= SlotSize<4>::kElems,
               "the epilogue's low, B^T, column-scale and bias tiles must fit in the slots they reuse");
 static_assert(STAGES * SlotSize<4>::kElems * 2 + 4096 * 4 <= 163840, "the slots and the largest tile map fit in LDS");
+static_assert(STAGES * SlotSize<4, kWNf4>::kElems * 2 + 4096 * 4 + 272 * 4 <= 163840, "the same with the NF4 code books");
+static_assert(WTile<kWNf4>::RowBytes * 2 == 64, "an NF4 stage is one block of 64 codes per row");
 
-template <bool BKC, int NRB>
+template <bool BKC, int NRB, int WT>
 static int launch_t(const GemmArgs& a, hipStream_t s) {
-  auto kern = grouped_gemm_bf16_kernel<BKC, NRB>;
-  const size_t lds = lds_bytes(a.E);
+  auto kern = grouped_gemm_bf16_kernel<BKC, NRB, WT>;
+  const size_t lds = lds_bytes(a.E, WT);
   static std::mutex mu;
   static std::unordered_map<int64_t, int> grid_cache;
   int dev = 0;
@@ -585,14 +726,14 @@ static int launch_t(const GemmArgs& a, hipStream_t s) {
   return launch_status("grouped_gemm");
 }
 
-template <bool BKC>
+template <bool BKC, int WT>
 static int launch_r(const GemmArgs& a, hipStream_t s) {
   switch (a.rank / 16) {
-    case 0: return launch_t<BKC, 0>(a, s);
-    case 1: return launch_t<BKC, 1>(a, s);
-    case 2: return launch_t<BKC, 2>(a, s);
-    case 3: return launch_t<BKC, 3>(a, s);
-    default: return launch_t<BKC, 4>(a, s);
+    case 0: return launch_t<BKC, 0, WT>(a, s);
+    case 1: return launch_t<BKC, 1, WT>(a, s);
+    case 2: return launch_t<BKC, 2, WT>(a, s);
+    case 3: return launch_t<BKC, 3, WT>(a, s);
+    default: return launch_t<BKC, 4, WT>(a, s);
   }
 }
 
@@ -600,7 +741,25 @@ static int launch_r(const GemmArgs& a, hipStream_t s) {
 
 int launch_grouped_gemm_bf16(const GemmArgs& a, bool k_contiguous, hipStream_t s) {
   if (a.scale_kind == MLORA_SCALE_ROW && a.scale_se == 0) return fail("grouped_gemm: per-row scale without a stride");
-  return k_contiguous ? dma::launch_r<true>(a, s) : dma::launch_r<false>(a, s);
+  return k_contiguous ? dma::launch_r<true, dma::kWBf16>(a, s) : dma::launch_r<false, dma::kWBf16>(a, s);
+}
+
+bool grouped_gemm_dma_takes(const GemmArgs& a, int w_dtype, bool k_contiguous, bool scale_on_k) {
+  // fp8 and NF4 stacks: k contiguous (each row copied as stored), rows of whole 16-byte chunks, a
+  // stack scale per expert or per output row (a scale along k stays with the register-staged kernel)
+  if (!k_contiguous || scale_on_k) return false;
+  if (w_dtype == MLORA_DT_FP8_E4M3)
+    return a.w_sn % 16 == 0 && a.w_se % 16 == 0 && ((uintptr_t)a.w & 15u) == 0;
+  if (w_dtype == MLORA_DT_NF4)  // rows of whole 64-code blocks (checked by the caller), 16-byte aligned packing
+    return a.w_sn % 64 == 0 && a.w_se % 64 == 0 && ((uintptr_t)a.w & 15u) == 0;
+  return false;
+}
+
+int launch_grouped_gemm_dma_q(const GemmArgs& a, int w_dtype, hipStream_t s) {
+  if (a.scale_kind == MLORA_SCALE_ROW && a.scale_se == 0) return fail("grouped_gemm: per-row scale without a stride");
+  if (w_dtype == MLORA_DT_FP8_E4M3) return dma::launch_r<true, dma::kWFp8>(a, s);
+  if (w_dtype == MLORA_DT_NF4) return dma::launch_r<true, dma::kWNf4>(a, s);
+  return fail("grouped_gemm: stack dtype %d has no DMA-fed product", w_dtype);
 }
 
 }  // namespace mlora

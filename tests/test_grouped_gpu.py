@@ -309,3 +309,33 @@ def test_the_gathered_product_is_bit_identical_to_the_product_of_the_gathered_ro
     g2 = (out2[:live].detach(), h2.grad, lhs.grad, rhs.grad)
     for name, a, b in zip(("out", "grad_h", "grad_lhs", "grad_rhs"), g1, g2):
         assert torch.equal(a, b), name
+
+
+@pytest.mark.parametrize("kind", ["fp8", "nf4"])
+@pytest.mark.parametrize("rank", [0, 16])
+def test_a_quantised_stack_in_the_forward_product_is_bit_identical_to_its_decoded_twin(kind, rank):
+    """fp8 e4m3 and NF4 stacks read with k contiguous are decoded in registers as the MFMA operands
+    are read, inside the same product as a bf16 stack: the result is the product of the decoded bf16
+    twin, to the bit (fp8 converted without a scale; NF4 blocks of 64 with their absmax)."""
+    from meepsquared_amd import _nf4, grouped_linear, lora_linear
+
+    torch.manual_seed(21 + rank)
+    rows_per_expert = [100, 0, 300, 37]
+    E, K, N = len(rows_per_expert), 256, 320
+    offsets = offsets_of(rows_per_expert)
+    x = torch.randn(sum(rows_per_expert), K, device="cuda").bfloat16()
+    w = torch.randn(E, N, K, device="cuda") * 0.05
+    if kind == "fp8":
+        stack = w.to(torch.float8_e4m3fn)
+        twin = stack.to(torch.bfloat16)
+    else:
+        stack = _nf4.quantize_stack(w)
+        twin = _nf4.dequantize_stack(stack, torch.bfloat16)
+    if rank == 0:
+        got = grouped_linear(x, stack, offsets, False, products_fp8=False)
+        want = grouped_linear(x, twin, offsets, False)
+    else:
+        lhs, rhs = torch.randn(E, N, rank, device="cuda").bfloat16() * 0.1, torch.randn(E, rank, K, device="cuda").bfloat16() * 0.1
+        got = lora_linear(x, stack, None, offsets, False, lhs, rhs, 2.0, products_fp8=False)
+        want = lora_linear(x, twin, None, offsets, False, lhs, rhs, 2.0)
+    assert torch.equal(got, want)
