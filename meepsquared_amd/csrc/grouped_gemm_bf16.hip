@@ -64,6 +64,8 @@ static_assert(FM >= 1 && FN >= 1 && (2 * FM) % WAVES_N == 0, "tile shape");
 
 typedef __attribute__((address_space(3))) void lds_void;
 
+constexpr int kSmallLastE = 1024;  // experts up to which the small last tiles are scheduled last
+
 // [row][k] tiles (rows of BK bf16, CPR chunks of 16 bytes): chunk c of row r in slot c ^ f(r), with f
 // spreading the 16 rows one MFMA operand read touches over 16 distinct 16-byte bank groups
 __device__ __forceinline__ int swz_f(int row) { return (row >> (CPR == 4 ? 2 : 1)) & (CPR - 1); }
@@ -95,50 +97,72 @@ __device__ __forceinline__ void stage_barrier() {
 // The tile map in LDS, one int per expert: tend[e] = the number of BM-row tiles of experts 0..e
 // (an inclusive scan; tend[E-1] is the tile count).  Expert e's rows are [start(e), start(e+1)) with
 // start(e) = offsets[e-1] clamped into [0, rows] (start(0) = 0), read from global memory when needed.
+// With small_last, an expert's last tile when it holds at most BM/2 rows is counted apart, in sfx[e]
+// (0 or 1, scanned the same way): those tiles are scheduled after all the others, so that they fill
+// the last rounds of the workgroups instead of landing at random (a near-empty tile still costs most
+// of a full one: its stages are bound by the copy latency).
 __device__ __forceinline__ int64_t row_start(const GemmArgs& p, int e) {
   if (e == 0) return 0;
   const int64_t o = p.offsets[e - 1];
   return o < 0 ? 0 : (o > p.rows ? p.rows : o);
 }
 
-__device__ __forceinline__ void build_tile_ends(const GemmArgs& p, int* tend, int tid) {
+__device__ __forceinline__ void scan_wave(int* v, int E, int lane) {  // inclusive scan by one wave
+  int run = 0;
+  for (int base = 0; base < E; base += 64) {
+    const int e = base + lane;
+    int incl = e < E ? v[e] : 0;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int u = __shfl_up(incl, o, 64);
+      if (lane >= o) incl += u;
+    }
+    if (e < E) v[e] = run + incl;
+    run += __shfl(incl, 63, 64);
+  }
+}
+
+__device__ __forceinline__ void build_tile_ends(const GemmArgs& p, int* tend, int* sfx, bool small_last, int tid) {
   const int E = p.E;
   for (int e = tid; e < E; e += kThreads) {
     const int64_t c = row_start(p, e + 1) - row_start(p, e);
-    tend[e] = c > 0 ? (int)((c + BM - 1) / BM) : 0;
+    const int nt = c > 0 ? (int)((c + BM - 1) / BM) : 0;
+    const int small = small_last && nt > 0 && c - (int64_t)(nt - 1) * BM <= BM / 2;
+    tend[e] = nt - small;
+    if (small_last) sfx[e] = small;
   }
   __syncthreads();
-  if (tid < 64) {  // inclusive scan by one wave, 64 experts at a time
-    const int lane = tid;
-    int run = 0;
-    for (int base = 0; base < E; base += 64) {
-      const int e = base + lane;
-      int incl = e < E ? tend[e] : 0;
-#pragma unroll
-      for (int o = 1; o < 64; o <<= 1) {
-        const int u = __shfl_up(incl, o, 64);
-        if (lane >= o) incl += u;
-      }
-      if (e < E) tend[e] = run + incl;
-      run += __shfl(incl, 63, 64);
-    }
-  }
+  if (tid < 64) scan_wave(tend, E, tid);
+  else if (small_last && tid < 128) scan_wave(sfx, E, tid - 64);
   __syncthreads();
 }
 
-// work item (tile t, column block) -> wave-uniform expert, rows and columns
-__device__ __forceinline__ Item decode(const GemmArgs& p, int64_t item, int nb, const int* tend) {
+__device__ __forceinline__ int first_above(const int* v, int E, int t) {  // the e with v[e-1] <= t < v[e]
+  int lo = 0, hi = E - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    if (v[mid] > t) hi = mid; else lo = mid + 1;
+  }
+  return __builtin_amdgcn_readfirstlane(lo);
+}
+
+// work item (tile t, column block) -> wave-uniform expert, rows and columns; small: t counts the
+// small last tiles
+__device__ __forceinline__ Item decode(const GemmArgs& p, int64_t item, int nb, const int* tend, const int* sfx,
+                                       bool small) {
   const int t = (int)(item / nb);
   Item it;
   it.nblk = (int)(item - (int64_t)t * nb);
-  int lo = 0, hi = p.E - 1;  // the expert e with tend[e-1] <= t < tend[e]
-  while (lo < hi) {
-    const int mid = (lo + hi) >> 1;
-    if (tend[mid] > t) hi = mid; else lo = mid + 1;
+  if (!small) {
+    it.e = first_above(tend, p.E, t);
+    const int t0 = it.e == 0 ? 0 : __builtin_amdgcn_readfirstlane(tend[it.e - 1]);
+    it.row0 = row_start(p, it.e) + (int64_t)(t - t0) * BM;
+  } else {
+    it.e = first_above(sfx, p.E, t);
+    const int big = __builtin_amdgcn_readfirstlane(tend[it.e]) -
+                    (it.e == 0 ? 0 : __builtin_amdgcn_readfirstlane(tend[it.e - 1]));
+    it.row0 = row_start(p, it.e) + (int64_t)big * BM;
   }
-  it.e = __builtin_amdgcn_readfirstlane(lo);
-  const int t0 = it.e == 0 ? 0 : __builtin_amdgcn_readfirstlane(tend[it.e - 1]);
-  it.row0 = row_start(p, it.e) + (int64_t)(t - t0) * BM;
   it.mrows = (int)min((int64_t)BM, row_start(p, it.e + 1) - it.row0);
   it.n0 = it.nblk * BN;
   return it;
@@ -482,28 +506,36 @@ __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_ker
   bf16* Ls = slot0;  // epilogue: [BM][LP] and [BN][LP], in slots the ring has finished with
   bf16* Lb = slot1;
 
-  // NF4: the code book (16) and the absmax code book (256) after the tile map
-  float* code = (float*)(tile_map + ((E + 3) & ~3));
+  // the small-tile counts after the tile map (experts up to kSmallLastE), then the NF4 code book (16)
+  // and absmax code book (256)
+  const bool small_last = E <= kSmallLastE;
+  int* sfx = tile_map + ((E + 3) & ~3);
+  float* code = (float*)(sfx + (small_last ? ((E + 3) & ~3) : 0));
   float off = 0.f;
   if constexpr (WT == kWNf4) {
     for (int c = tid0; c < 16 + 256; c += kThreads) code[c] = c < 16 ? p.nf4_code[c] : p.nf4_code2[c - 16];
     off = p.nf4_offset[0];
   }
-  build_tile_ends(p, tile_map, tid0);
+  build_tile_ends(p, tile_map, sfx, small_last, tid0);
   const int nb = (p.N + BN - 1) / BN;
-  const int64_t total = (int64_t)__builtin_amdgcn_readfirstlane(tile_map[E - 1]) * nb;
+  // each XCD takes one contiguous eighth of the full tiles' items, then one eighth of the small tiles'
+  const int64_t nbig = (int64_t)__builtin_amdgcn_readfirstlane(tile_map[E - 1]) * nb;
+  const int64_t nsmall = small_last ? (int64_t)__builtin_amdgcn_readfirstlane(sfx[E - 1]) * nb : 0;
   const int xcd = blockIdx.x % kXcds, wg_slot = blockIdx.x / kXcds, per_xcd = gridDim.x / kXcds;
-  const int64_t chunk = (total + kXcds - 1) / kXcds;
-  const int64_t beg = xcd * chunk, end = min(beg + chunk, total);
+  const int64_t cbig = (nbig + kXcds - 1) / kXcds, csmall = (nsmall + kXcds - 1) / kXcds;
+  const int64_t bbeg = min(xcd * cbig, nbig), bcnt = min(bbeg + cbig, nbig) - bbeg;
+  const int64_t sbeg = min(xcd * csmall, nsmall), scnt = min(sbeg + csmall, nsmall) - sbeg;
   const int nk = (p.K + BK - 1) / BK;
 
-  for (int64_t item = beg + wg_slot; item < end; item += per_xcd) {
+  for (int64_t j = wg_slot; j < bcnt + scnt; j += per_xcd) {
+    const bool small = j >= bcnt;
+    const int64_t item = small ? sbeg + (j - bcnt) : bbeg + j;
     // the thread index taken afresh for every item: values derived from it are computed where they
     // are used, not hoisted out of this loop to hold registers through every K loop and epilogue
     int tid = tid0;
     asm volatile("" : "+v"(tid));
     const int lane = tid & 63;
-    const Item it = decode(p, item, nb, tile_map);
+    const Item it = decode(p, item, nb, tile_map, sfx, small);
     const int e = it.e, n0 = it.n0, mrows = it.mrows;
     const int64_t row0 = it.row0;
     const int ncols = min(BN, p.N - n0);
@@ -686,12 +718,16 @@ __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_ker
   }
 }
 
-static size_t lds_bytes(int E, int WT) { return (size_t)((E + 3) & ~3) * sizeof(int) + (WT == kWNf4 ? 272 * 4 : 0); }
+static size_t lds_bytes(int E, int WT) {
+  const size_t ea = (size_t)((E + 3) & ~3);
+  return ea * sizeof(int) * (E <= kSmallLastE ? 2 : 1) + (WT == kWNf4 ? 272 * 4 : 0);
+}
 static_assert(BM * (kMaxRank + 8) <= SlotSize<4>::kElems &&
                   BN * (kMaxRank + 8) + (STAGES == 4 ? 0 : BN * 3) <= SlotSize<4>::kElems,
               "the epilogue's low, B^T, column-scale and bias tiles must fit in the slots they reuse");
 static_assert(STAGES * SlotSize<4>::kElems * 2 + 4096 * 4 <= 163840, "the slots and the largest tile map fit in LDS");
 static_assert(STAGES * SlotSize<4, kWNf4>::kElems * 2 + 4096 * 4 + 272 * 4 <= 163840, "the same with the NF4 code books");
+static_assert(STAGES * SlotSize<4>::kElems * 2 + kSmallLastE * 8 <= 163840, "the small-tile counts fit beside the slots");
 static_assert(WTile<kWNf4>::RowBytes * 2 == 64, "an NF4 stage is one block of 64 codes per row");
 
 template <bool BKC, int NRB, int WT>
