@@ -181,6 +181,11 @@ def _launch(x, weight, scale, offsets, is_transposed, adapters, scaling, bias, s
         if weight.dtype not in (torch.bfloat16, torch.float8_e4m3fn):
             raise TypeError(f"a stack in {weight.dtype}: the kernel takes bf16, float8_e4m3fn or NF4")
         w_ptr, w_dtype = ptr(weight), _lib.dtype_code(weight.dtype)
+        if weight.dtype == torch.float8_e4m3fn and w_sk != 1 and w_sn == 1:
+            # an fp8 stack read with n contiguous: its k-contiguous byte copy (kept on the stack), which the
+            # DMA-fed product decodes in registers
+            w8, w_se, w_sn = _k_contiguous(weight, w_se, w_sk, w_sn, K, N)
+            w_sk, w_ptr = 1, ptr(w8)
     if bias is not None:
         bias = bias.to(torch.bfloat16)
         if bias.stride(-1) != 1:

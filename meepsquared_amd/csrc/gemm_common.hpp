@@ -129,6 +129,6 @@ __device__ __forceinline__ Item decode_item(int64_t item, int nb, int E, int bm,
 int launch_grouped_gemm_bf16(const GemmArgs& a, bool k_contiguous, hipStream_t s);
 // the DMA-fed product for a quantised stack read with k contiguous (decoded in registers)
 bool grouped_gemm_dma_takes(const GemmArgs& a, int w_dtype, bool k_contiguous, bool scale_on_k);
-int launch_grouped_gemm_dma_q(const GemmArgs& a, int w_dtype, hipStream_t s);
+int launch_grouped_gemm_dma_q(const GemmArgs& a, int w_dtype, bool scale_on_k, hipStream_t s);
 
 }  // namespace mlora

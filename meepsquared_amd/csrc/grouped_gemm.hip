@@ -666,11 +666,11 @@ static int grouped_gemm_impl(const void* x, int64_t ldx, const int64_t* gather, 
   switch (w_dtype) {
     case MLORA_DT_BF16: return launch_grouped_gemm_bf16(g, bkc, s);
     case MLORA_DT_FP8_E4M3:
-      if (grouped_gemm_dma_takes(g, w_dtype, bkc, scale_k)) return launch_grouped_gemm_dma_q(g, w_dtype, s);
+      if (grouped_gemm_dma_takes(g, w_dtype, bkc, scale_k)) return launch_grouped_gemm_dma_q(g, w_dtype, scale_k, s);
       if (scale_k) return bkc ? launch_r<W_FP8, true, true>(g, s) : launch_r<W_FP8, false, true>(g, s);
       return bkc ? launch_r<W_FP8, true, false>(g, s) : launch_r<W_FP8, false, false>(g, s);
     default:
-      if (grouped_gemm_dma_takes(g, w_dtype, bkc, false)) return launch_grouped_gemm_dma_q(g, w_dtype, s);
+      if (grouped_gemm_dma_takes(g, w_dtype, bkc, false)) return launch_grouped_gemm_dma_q(g, w_dtype, false, s);
       return bkc ? launch_r<W_NF4, true, false>(g, s) : launch_r<W_NF4, false, false>(g, s);
   }
 }

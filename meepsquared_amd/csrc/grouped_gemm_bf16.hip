@@ -175,18 +175,24 @@ __device__ __forceinline__ Item decode(const GemmArgs& p, int64_t item, int nb, 
 // waves in whole runs of lanes (rank 48 is copied as 64 rows, the last 16 read as zeros).
 // The stack's element type in LDS: bf16, or fp8 e4m3 / NF4 copied as stored (k contiguous) and
 // decoded to bf16 in registers as each MFMA operand is read.
-enum : int { kWBf16 = 0, kWFp8 = 1, kWNf4 = 2 };
+// kWFp8K: fp8 with a per-row stack scale that lies along k here (the input-gradient product of a
+// stack with one scale per output row, read through its k-contiguous copy): the stage's BK scales are
+// copied beside the tile and applied in the decode, bf16(e4m3 · s_k), as the register-staged kernel does.
+enum : int { kWBf16 = 0, kWFp8 = 1, kWNf4 = 2, kWFp8K = 3 };
 template <int WT>
 struct WTile {
-  static constexpr int RowBytes = WT == kWBf16 ? BK * 2 : WT == kWFp8 ? BK : BK / 2;  // one row of the stage
+  static constexpr bool kFp8 = WT == kWFp8 || WT == kWFp8K;
+  static constexpr int RowBytes = WT == kWBf16 ? BK * 2 : kFp8 ? BK : BK / 2;         // one row of the stage
   static constexpr int Chunks = RowBytes / 16;                                         // 16-byte chunks per row
-  static constexpr int Elems = BN * RowBytes / 2;                                      // bf16 slots of LDS
+  static constexpr int Bytes = BN * RowBytes;                                          // the tile
+  static constexpr int Elems = Bytes / 2 + (WT == kWFp8K ? BK * 2 : 0);                // bf16 slots of LDS (+ scales)
   static constexpr int WI = BN * Chunks / (64 * NW);                                   // copies per wave
   static_assert(BN * Chunks % (64 * NW) == 0, "the stack tile splits evenly over the waves");
+  static_assert(WT != kWFp8K || BK == 64, "one dword copy of 64 lanes carries a stage's scales");
 };
 // [n][k] byte tiles of fp8 (4 chunks per row) and NF4 (2): chunk c of row n in slot c ^ g(n)
 template <int WT>
-__device__ __forceinline__ int swz_q(int n) { return WT == kWFp8 ? (n >> 2) & 3 : (n >> 3) & 1; }
+__device__ __forceinline__ int swz_q(int n) { return WTile<WT>::kFp8 ? (n >> 2) & 3 : (n >> 3) & 1; }
 
 template <int NRB, int WT = kWBf16>
 struct SlotSize {
@@ -205,14 +211,16 @@ struct Feed {
   static constexpr int WI = WTile<WT>::WI;
   // this wave's copies per stage: XI of x, WI of the stack, one (lane-masked) of A^T
   static constexpr int PS = XI + WI + (NRB > 0 ? 1 : 0);
-  rsrc_t rx, rw, ra;
+  rsrc_t rx, rw, ra, rs;  // rs: the expert's scales along k (kWFp8K)
   uint32_t xo[XI], wo[WI], ao;
   int xk[XI], wk[WI], ak;
   int xd[XI], wd[WI], ad;  // LDS element offset of each instruction's 64 lanes within the slot
   bool a_on;
+  int lane_;
   int64_t wstep;           // bytes the stack offset advances per k (BKC: 2; else 2 * w_sk)
 
   __device__ __forceinline__ void init(const GemmArgs& p, int n0, int64_t row0, int mrows, int wave, int lane) {
+    lane_ = lane;
 #pragma unroll
     for (int q = 0; q < XI; ++q) {
       const int instr = wave * XI + q, ci = instr * 64 + lane;
@@ -233,9 +241,9 @@ struct Feed {
         constexpr int CH = WTile<WT>::Chunks;
         const int row = ci / CH, c = (ci % CH) ^ swz_q<WT>(row);
         const int n = n0 + row;
-        const int64_t rowb = WT == kWFp8 ? (int64_t)n * p.w_sn : (int64_t)n * p.w_sn / 2;
+        const int64_t rowb = WTile<WT>::kFp8 ? (int64_t)n * p.w_sn : (int64_t)n * p.w_sn / 2;
         wo[q] = n < p.N ? (uint32_t)(rowb + c * 16) : 0u;
-        wk[q] = n < p.N ? c * (WT == kWFp8 ? 16 : 32) : (1 << 30);
+        wk[q] = n < p.N ? c * (WTile<WT>::kFp8 ? 16 : 32) : (1 << 30);
       } else if constexpr (BKC) {  // [n][k]
         const int row = ci / CPR, c = (ci % CPR) ^ swz_f(row);
         const int n = n0 + row;
@@ -249,7 +257,7 @@ struct Feed {
       }
       wd[q] = BM * BK + instr * 512;
     }
-    wstep = WT == kWFp8 ? 1 : BKC ? 2 : 2 * p.w_sk;
+    wstep = WTile<WT>::kFp8 ? 1 : BKC ? 2 : 2 * p.w_sk;
     if constexpr (NRB > 0) {
       // wave w copies chunks [w * CPW, (w + 1) * CPW) of the A^T tile: lanes of one 64-chunk
       // instruction block, the others masked off (their LDS bytes belong to other waves)
@@ -276,13 +284,36 @@ struct Feed {
     if constexpr (NRB > 0) {
       if (a_on) dma16(ra, slot + ad, ak + k0 < p.K ? ao + (uint32_t)(k0 * 2) : kOob);
     }
+    if constexpr (WT == kWFp8K) {  // every wave copies the same 64 scales (one dword per lane)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(slot + BM * BK + WTile<WT>::Bytes / 2), 4,
+                                               k0 + lane_ < p.K ? (uint32_t)((k0 + lane_) * 4) : kOob, 0, 0, 0);
+    }
   }
 };
 
 // the stack's fragment for MFMA (32 columns n at nb, 8 consecutive k at kb + 8*(lane/32))
 template <bool BKC, int WT = kWBf16>
 __device__ __forceinline__ bf16x8 w_frag(const bf16* bs, int nb, int kk, int lane) {
-  if constexpr (WT == kWFp8) {
+  if constexpr (WT == kWFp8K) {
+    // as kWFp8, each value then multiplied by its k's scale in fp32 and rounded once to bf16
+    const int n = nb + (lane & 31);
+    const u32x2 v = *(const u32x2*)((const uint8_t*)bs + n * BK + ((kk ^ swz_q<WT>(n)) << 4) + 8 * (lane >> 5));
+    const float* sc = (const float*)((const uint8_t*)bs + WTile<WT>::Bytes) + kk * 16 + 8 * (lane >> 5);
+    const f32x4 s0 = *(const f32x4*)sc, s1 = *(const f32x4*)(sc + 4);
+    const unsigned d[4] = {__builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(v[0], 1.f, false)),
+                           __builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(v[0], 1.f, true)),
+                           __builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(v[1], 1.f, false)),
+                           __builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(v[1], 1.f, true))};
+    unsigned w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float a = bf16_bits_to_f32(d[i] & 0xFFFFu), b = bf16_bits_to_f32(d[i] >> 16);
+      const float sa = i < 2 ? s0[2 * i] : s1[2 * i - 4], sb = i < 2 ? s0[2 * i + 1] : s1[2 * i - 3];
+      w[i] = pack_bf16x2(a * sa, b * sb);
+    }
+    typedef unsigned u32x4_ __attribute__((ext_vector_type(4)));
+    return __builtin_bit_cast(bf16x8, (u32x4_{w[0], w[1], w[2], w[3]}));
+  } else if constexpr (WT == kWFp8) {
     // eight e4m3 bytes of row n (16-byte chunk kk, half lane/32), converted exactly to bf16
     const int n = nb + (lane & 31);
     const u32x2 v = *(const u32x2*)((const uint8_t*)bs + n * BK + ((kk ^ swz_q<WT>(n)) << 4) + 8 * (lane >> 5));
@@ -547,8 +578,9 @@ __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_ker
     f.rx = p.gather == nullptr ? make_rsrc(p.x + row0 * p.ldx, (int64_t)mrows * p.ldx * 2)
                                : make_rsrc(p.x, p.xrows * p.ldx * 2);
     {
-      const int64_t ebytes = WT == kWBf16 ? p.w_se * 2 : WT == kWFp8 ? p.w_se : p.w_se / 2;  // one expert's stack
+      const int64_t ebytes = WT == kWBf16 ? p.w_se * 2 : WTile<WT>::kFp8 ? p.w_se : p.w_se / 2;  // one expert's stack
       f.rw = make_rsrc(p.w + (int64_t)e * ebytes, ebytes);
+      if constexpr (WT == kWFp8K) f.rs = make_rsrc(p.scale + (int64_t)e * p.scale_se, (int64_t)p.K * 4);
     }
     f.ra = f.rx;
     if constexpr (NRB > 0) f.ra = make_rsrc(p.at + (int64_t)e * p.at_se, (int64_t)RP * p.at_sr * 2);
@@ -599,7 +631,7 @@ __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_ker
     // [BN] per-column stack scale (MLORA_SCALE_ROW) and [BN] bias: after B^T, or in the third slot
     float* Lc = (float*)(STAGES == 4 ? slots[STAGES - 2] : Lb + BN * LP);
     bf16* Lbias = (bf16*)(Lc + BN);      // [BN] bias
-    const bool col_scale = p.scale_kind == MLORA_SCALE_ROW, has_bias = p.bias != nullptr;
+    const bool col_scale = p.scale_kind == MLORA_SCALE_ROW && WT != kWFp8K, has_bias = p.bias != nullptr;
     const float cexp = p.scale_kind == MLORA_SCALE_EXPERT ? p.scale[e] : 1.f;
     if (tid < BN && (col_scale || has_bias)) {
       const int n = n0 + tid;
@@ -783,16 +815,19 @@ int launch_grouped_gemm_bf16(const GemmArgs& a, bool k_contiguous, hipStream_t s
 bool grouped_gemm_dma_takes(const GemmArgs& a, int w_dtype, bool k_contiguous, bool scale_on_k) {
   // fp8 and NF4 stacks: k contiguous (each row copied as stored), rows of whole 16-byte chunks, a
   // stack scale per expert or per output row (a scale along k stays with the register-staged kernel)
-  if (!k_contiguous || scale_on_k) return false;
+  if (!k_contiguous) return false;
   if (w_dtype == MLORA_DT_FP8_E4M3)
-    return a.w_sn % 16 == 0 && a.w_se % 16 == 0 && ((uintptr_t)a.w & 15u) == 0;
+    return a.w_sn % 16 == 0 && a.w_se % 16 == 0 && ((uintptr_t)a.w & 15u) == 0 &&
+           (!scale_on_k || (a.scale_kind == MLORA_SCALE_ROW && a.scale_se % 4 == 0 && ((uintptr_t)a.scale & 15u) == 0));
+  if (scale_on_k) return false;
   if (w_dtype == MLORA_DT_NF4)  // rows of whole 64-code blocks (checked by the caller), 16-byte aligned packing
     return a.w_sn % 64 == 0 && a.w_se % 64 == 0 && ((uintptr_t)a.w & 15u) == 0;
   return false;
 }
 
-int launch_grouped_gemm_dma_q(const GemmArgs& a, int w_dtype, hipStream_t s) {
+int launch_grouped_gemm_dma_q(const GemmArgs& a, int w_dtype, bool scale_on_k, hipStream_t s) {
   if (a.scale_kind == MLORA_SCALE_ROW && a.scale_se == 0) return fail("grouped_gemm: per-row scale without a stride");
+  if (w_dtype == MLORA_DT_FP8_E4M3 && scale_on_k) return dma::launch_r<true, dma::kWFp8K>(a, s);
   if (w_dtype == MLORA_DT_FP8_E4M3) return dma::launch_r<true, dma::kWFp8>(a, s);
   if (w_dtype == MLORA_DT_NF4) return dma::launch_r<true, dma::kWNf4>(a, s);
   return fail("grouped_gemm: stack dtype %d has no DMA-fed product", w_dtype);

@@ -339,3 +339,32 @@ def test_a_quantised_stack_in_the_forward_product_is_bit_identical_to_its_decode
         got = lora_linear(x, stack, None, offsets, False, lhs, rhs, 2.0, products_fp8=False)
         want = lora_linear(x, twin, None, offsets, False, lhs, rhs, 2.0)
     assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("is_transposed", [False, True])
+def test_the_input_gradient_through_an_fp8_stack_is_bit_identical_to_its_decoded_twin(is_transposed):
+    """An fp8 stack with one scale per output row, products in bf16: the input-gradient product reads the
+    stack with k contiguous (directly, or through its byte-transposed copy) and applies each row's scale
+    along k in the decode, bf16(e4m3 · s): the gradient is that of the scaled bf16 twin, to the bit."""
+    from meepsquared_amd import _fp8, lora_linear
+
+    torch.manual_seed(5)
+    rows_per_expert = [100, 0, 300, 37]
+    E, K, N, r = len(rows_per_expert), 256, 320, 16
+    offsets = offsets_of(rows_per_expert)
+    w = (torch.randn((E, K, N) if is_transposed else (E, N, K), device="cuda") * 0.05).bfloat16()
+    stack, scale = _fp8.quantize_stack(w, per_row=True, is_transposed=is_transposed)
+    twin = (stack.float() * (scale[:, None, :] if is_transposed else scale[:, :, None])).bfloat16()
+    if is_transposed:
+        lhs, rhs = torch.randn(E, K, r, device="cuda") * 0.1, torch.randn(E, r, N, device="cuda") * 0.1
+    else:
+        lhs, rhs = torch.randn(E, N, r, device="cuda") * 0.1, torch.randn(E, r, K, device="cuda") * 0.1
+    x = torch.randn(sum(rows_per_expert), K, device="cuda").bfloat16()
+    dy = torch.randn(sum(rows_per_expert), N, device="cuda").bfloat16()
+    grads = []
+    for wt, sc in ((stack, scale), (twin, None)):
+        xx = x.clone().requires_grad_()
+        out = lora_linear(xx, wt, sc, offsets, is_transposed, lhs.bfloat16(), rhs.bfloat16(), 2.0, products_fp8=False)
+        out.backward(dy)
+        grads.append(xx.grad)
+    assert torch.equal(grads[0], grads[1])
