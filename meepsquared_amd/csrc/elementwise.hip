@@ -181,6 +181,32 @@ __global__ __launch_bounds__(256) void combine_backward_kernel(const u32x4* __re
   }
 }
 
+// The combine weights' gradient alone (the down product then reads the output gradient through the
+// permutation, so no weighted copy dy is written): one wave per (token, slot), dw = <dout[t], y[p]>,
+// fp32 lane sums then a wave sum; no barrier.
+template <typename TW>
+__global__ __launch_bounds__(256) void combine_dw_kernel(const u32x4* __restrict__ dout, const u32x4* __restrict__ y,
+                                                         int64_t Hv, const int64_t* __restrict__ inv, int64_t T, int k,
+                                                         const int32_t* __restrict__ offsets, int E,
+                                                         TW* __restrict__ dw) {
+  const int64_t idx = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (idx >= T * k) return;  // whole waves
+  const int lane = threadIdx.x & 63;
+  const int64_t t = idx / k, p = inv[idx];
+  float dot = 0.f;
+  if (p < offsets[E - 1]) {
+    for (int64_t c = lane; c < Hv; c += 64) {
+      float d[8], f[8];
+      unpack8(dout[t * Hv + c], d);
+      unpack8(y[p * Hv + c], f);
+#pragma unroll
+      for (int q = 0; q < 8; ++q) dot += d[q] * f[q];
+    }
+  }
+  dot = wave_sum(dot);
+  if (lane == 0) dw[idx] = (TW)dot;
+}
+
 static unsigned grid_for(int64_t total) {
   int64_t g = (total + 255) / 256;
   if (g > 256 * 64) g = 256 * 64;
@@ -257,6 +283,19 @@ extern "C" int mlora_combine_backward(const void* dout, const void* y, int64_t H
   if (k < 1 || E < 1) return fail("combine_backward: k=%d, E=%d must be >= 1", k, E);
   if (T == 0) return 0;
   if (T > 0x7FFFFFFF) return fail("combine_backward: T=%lld too large", (long long)T);
+  if (dy == nullptr) {
+    const int64_t blocks = (T * k + 3) / 4;
+    if (blocks > 0x7FFFFFFF) return fail("combine_backward: T*k=%lld too large", (long long)(T * k));
+    if (w_dtype == MLORA_DT_F32)
+      hipLaunchKernelGGL(combine_dw_kernel<float>, dim3((unsigned)blocks), dim3(256), 0, as_stream(stream),
+                         (const u32x4*)dout, (const u32x4*)y, H / 8, inv, T, k, offsets, E, (float*)dw);
+    else if (w_dtype == MLORA_DT_BF16)
+      hipLaunchKernelGGL(combine_dw_kernel<bf16>, dim3((unsigned)blocks), dim3(256), 0, as_stream(stream),
+                         (const u32x4*)dout, (const u32x4*)y, H / 8, inv, T, k, offsets, E, (bf16*)dw);
+    else
+      return fail("combine_backward: weight dtype %d is not bf16/f32", w_dtype);
+    return launch_status("combine_backward");
+  }
   const dim3 g((unsigned)T), b(256);
   if (w_dtype == MLORA_DT_F32)
     hipLaunchKernelGGL(combine_backward_kernel<float>, g, b, 0, as_stream(stream), (const u32x4*)dout,
