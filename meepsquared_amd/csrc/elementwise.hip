@@ -48,23 +48,38 @@ __global__ __launch_bounds__(256) void gather_rows_kernel(const u32x4* __restric
 }
 
 // ---- the gather's gradient: per token, the sum of its k rows ----
+// Rows summed or weighted per token over its k slots: with k known at compile time (KT > 0) the slot
+// loop is unrolled, so every slot's index and row loads are in flight together.
+template <int KT, typename F>
+__device__ __forceinline__ void for_slots(int k, F&& f) {
+  if constexpr (KT > 0) {
+#pragma unroll
+    for (int j = 0; j < KT; ++j) f(j);
+  } else {
+    for (int j = 0; j < k; ++j) f(j);
+  }
+}
+
+template <int KT>
 __global__ __launch_bounds__(256) void gather_rows_backward_kernel(const u32x4* __restrict__ dsel, int64_t Hv,
                                                                    const int64_t* __restrict__ inv, int64_t T, int k,
                                                                    const int32_t* __restrict__ offsets, int E,
                                                                    u32x4* __restrict__ dh) {
+  if constexpr (KT > 0) k = KT;
   const int64_t valid = offsets[E - 1];
   const int64_t total = T * Hv;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
     const int64_t t = i / Hv, c = i - t * Hv;
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int j = 0; j < k; ++j) {
+    for_slots<KT>(k, [&](int j) {
       const int64_t p = inv[t * k + j];
-      if (p >= valid) continue;
-      float f[8];
-      unpack8(dsel[p * Hv + c], f);
+      if (p < valid) {
+        float f[8];
+        unpack8(dsel[p * Hv + c], f);
 #pragma unroll
-      for (int q = 0; q < 8; ++q) acc[q] += f[q];
-    }
+        for (int q = 0; q < 8; ++q) acc[q] += f[q];
+      }
+    });
     dh[i] = pack8(acc);
   }
 }
@@ -109,30 +124,32 @@ __global__ __launch_bounds__(256) void swiglu_backward_kernel(const u32x4* __res
 }
 
 // ---- combine: per token, sum over its k rows of bf16(y * w) ----
-template <typename TW>
+template <int KT, typename TW>
 __global__ __launch_bounds__(256) void combine_kernel(const u32x4* __restrict__ y, int64_t Hv,
                                                       const TW* __restrict__ w, const int64_t* __restrict__ inv,
                                                       int64_t T, int k, const int32_t* __restrict__ offsets, int E,
                                                       u32x4* __restrict__ out) {
   constexpr bool kBf16Weights = sizeof(TW) == 2;
+  if constexpr (KT > 0) k = KT;
   const int64_t valid = offsets[E - 1];
   const int64_t total = T * Hv;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
     const int64_t t = i / Hv, c = i - t * Hv;
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int j = 0; j < k; ++j) {
+    for_slots<KT>(k, [&](int j) {
       const int64_t p = inv[t * k + j];
-      if (p >= valid) continue;
-      const float wt = load_w(w, t * k + j);
-      float f[8];
-      unpack8(y[p * Hv + c], f);
+      if (p < valid) {
+        const float wt = load_w(w, t * k + j);
+        float f[8];
+        unpack8(y[p * Hv + c], f);
 #pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        // with bf16 weights the reference's product is a bf16 tensor; with fp32 weights it is fp32
-        const float prod = f[q] * wt;
-        acc[q] += kBf16Weights ? round_bf16(prod) : prod;
+        for (int q = 0; q < 8; ++q) {
+          // with bf16 weights the reference's product is a bf16 tensor; with fp32 weights it is fp32
+          const float prod = f[q] * wt;
+          acc[q] += kBf16Weights ? round_bf16(prod) : prod;
+        }
       }
-    }
+    });
     out[i] = pack8(acc);
   }
 }
@@ -234,8 +251,19 @@ extern "C" int mlora_gather_rows_backward(const void* dsel, int64_t H, const int
   if (H % 8) return fail("gather_rows_backward: H=%lld must be a multiple of 8", (long long)H);
   if (k < 1 || E < 1) return fail("gather_rows_backward: k=%d, E=%d must be >= 1", k, E);
   if (T == 0) return 0;
-  hipLaunchKernelGGL(gather_rows_backward_kernel, dim3(grid_for(T * (H / 8))), dim3(256), 0, as_stream(stream),
-                     (const u32x4*)dsel, H / 8, inv, T, k, offsets, E, (u32x4*)dh);
+  const dim3 g(grid_for(T * (H / 8))), b(256);
+#define MLORA_GRB(KT)                                                                                      \
+  hipLaunchKernelGGL(gather_rows_backward_kernel<KT>, g, b, 0, as_stream(stream), (const u32x4*)dsel, H / 8, inv, T, \
+                     k, offsets, E, (u32x4*)dh)
+  switch (k) {
+    case 1: MLORA_GRB(1); break;
+    case 2: MLORA_GRB(2); break;
+    case 4: MLORA_GRB(4); break;
+    case 6: MLORA_GRB(6); break;
+    case 8: MLORA_GRB(8); break;
+    default: MLORA_GRB(0); break;
+  }
+#undef MLORA_GRB
   return launch_status("gather_rows_backward");
 }
 
@@ -264,14 +292,23 @@ extern "C" int mlora_combine(const void* y, int64_t H, const void* w, int w_dtyp
   if (k < 1 || E < 1) return fail("combine: k=%d, E=%d must be >= 1", k, E);
   if (T == 0) return 0;
   const dim3 g(grid_for(T * (H / 8))), b(256);
-  if (w_dtype == MLORA_DT_F32)
-    hipLaunchKernelGGL(combine_kernel<float>, g, b, 0, as_stream(stream), (const u32x4*)y, H / 8, (const float*)w,
-                       inv, T, k, offsets, E, (u32x4*)out);
-  else if (w_dtype == MLORA_DT_BF16)
-    hipLaunchKernelGGL(combine_kernel<bf16>, g, b, 0, as_stream(stream), (const u32x4*)y, H / 8, (const bf16*)w, inv,
-                       T, k, offsets, E, (u32x4*)out);
-  else
-    return fail("combine: weight dtype %d is not bf16/f32", w_dtype);
+  if (w_dtype != MLORA_DT_F32 && w_dtype != MLORA_DT_BF16) return fail("combine: weight dtype %d is not bf16/f32", w_dtype);
+#define MLORA_CMB(KT)                                                                                          \
+  if (w_dtype == MLORA_DT_F32)                                                                                 \
+    hipLaunchKernelGGL((combine_kernel<KT, float>), g, b, 0, as_stream(stream), (const u32x4*)y, H / 8,         \
+                       (const float*)w, inv, T, k, offsets, E, (u32x4*)out);                                   \
+  else                                                                                                         \
+    hipLaunchKernelGGL((combine_kernel<KT, bf16>), g, b, 0, as_stream(stream), (const u32x4*)y, H / 8,          \
+                       (const bf16*)w, inv, T, k, offsets, E, (u32x4*)out)
+  switch (k) {
+    case 1: MLORA_CMB(1); break;
+    case 2: MLORA_CMB(2); break;
+    case 4: MLORA_CMB(4); break;
+    case 6: MLORA_CMB(6); break;
+    case 8: MLORA_CMB(8); break;
+    default: MLORA_CMB(0); break;
+  }
+#undef MLORA_CMB
   return launch_status("combine");
 }
 

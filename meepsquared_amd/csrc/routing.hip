@@ -37,7 +37,7 @@ __device__ __forceinline__ float key_value(uint64_t key) {
 
 constexpr int kTopkMaxPerLane = 16;  // E <= 1024
 
-template <typename TL, typename TW>
+template <typename TL, typename TW, int PL>  // PL: logits per lane, ceil(E / 64)
 __global__ __launch_bounds__(256) void topk_softmax_kernel(const TL* __restrict__ logits, int64_t ld, int64_t T,
                                                            int E, int k, int renorm, int64_t* __restrict__ out_idx,
                                                            TW* __restrict__ out_w) {
@@ -45,10 +45,10 @@ __global__ __launch_bounds__(256) void topk_softmax_kernel(const TL* __restrict_
   const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
   const TL* row = logits + t * ld;
-  float v[kTopkMaxPerLane];
+  float v[PL];
   float m = -INFINITY;
 #pragma unroll
-  for (int i = 0; i < kTopkMaxPerLane; ++i) {
+  for (int i = 0; i < PL; ++i) {
     const int e = lane + 64 * i;
     v[i] = (e < E) ? load_logit(row + e) : -INFINITY;
     m = fmaxf(m, v[i]);
@@ -56,7 +56,7 @@ __global__ __launch_bounds__(256) void topk_softmax_kernel(const TL* __restrict_
   m = wave_max(m);
   float z = 0.f;
 #pragma unroll
-  for (int i = 0; i < kTopkMaxPerLane; ++i) {
+  for (int i = 0; i < PL; ++i) {
     const int e = lane + 64 * i;
     if (e < E) z += expf(v[i] - m);
   }
@@ -68,7 +68,7 @@ __global__ __launch_bounds__(256) void topk_softmax_kernel(const TL* __restrict_
   for (int j = 0; j < k; ++j) {
     uint64_t best = 0;
 #pragma unroll
-    for (int i = 0; i < kTopkMaxPerLane; ++i) {
+    for (int i = 0; i < PL; ++i) {
       const int e = lane + 64 * i;
       if (e < E && !((taken >> i) & 1u)) {
         uint64_t key = rank_key(v[i], e);
@@ -302,9 +302,17 @@ extern "C" int mlora_route_topk(const void* logits, int logits_dtype, int64_t ld
   if (T == 0) return 0;
   const dim3 grid((unsigned)((T + 3) / 4)), block(256);
   hipStream_t s = as_stream(stream);
+#define MLORA_TOPK_PL(TL, TW, PL)                                                                        \
+  hipLaunchKernelGGL((topk_softmax_kernel<TL, TW, PL>), grid, block, 0, s, (const TL*)logits, ld_logits, T, E, \
+                     k, renorm, out_idx, (TW*)out_w)
 #define MLORA_TOPK(TL, TW)                                                                                     \
-  hipLaunchKernelGGL((topk_softmax_kernel<TL, TW>), grid, block, 0, s, (const TL*)logits, ld_logits, T, E, k, \
-                     renorm, out_idx, (TW*)out_w)
+  do {                                                                                                         \
+    if (E <= 64) MLORA_TOPK_PL(TL, TW, 1);                                                                     \
+    else if (E <= 128) MLORA_TOPK_PL(TL, TW, 2);                                                               \
+    else if (E <= 256) MLORA_TOPK_PL(TL, TW, 4);                                                               \
+    else if (E <= 512) MLORA_TOPK_PL(TL, TW, 8);                                                               \
+    else MLORA_TOPK_PL(TL, TW, kTopkMaxPerLane);                                                               \
+  } while (0)
   if (w_dtype != MLORA_DT_BF16 && w_dtype != MLORA_DT_F32) return fail("route_topk: w_dtype %d is not bf16/f32", w_dtype);
   const bool wf = w_dtype == MLORA_DT_F32;
   switch (logits_dtype) {
@@ -314,6 +322,7 @@ extern "C" int mlora_route_topk(const void* logits, int logits_dtype, int64_t ld
     default: return fail("route_topk: logits dtype %d is not bf16/f16/f32", logits_dtype);
   }
 #undef MLORA_TOPK
+#undef MLORA_TOPK_PL
   return launch_status("route_topk");
 }
 
