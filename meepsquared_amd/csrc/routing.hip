@@ -188,13 +188,28 @@ __device__ __forceinline__ uint64_t same_bin(int bin, int nbits) {
   return m;
 }
 
-// Per-wave histogram of the wave's 1024 ids into cnt[0..E] (bin E = sentinels); bin E+1 marks lanes
-// past the end of the ids and is not counted.
-__device__ void wave_histogram(const int64_t* ids, int64_t S, int E, int nbits, int64_t base, int* cnt) {
+// The bins of this lane's ids in the wave's 1024 (all loaded before any is used: one memory round
+// trip, not one per sub-chunk); bin E+1 marks lanes past the end of the ids.
+__device__ __forceinline__ void load_bins(const int64_t* ids, int64_t S, int E, int64_t base, int (&bins)[kSortSub]) {
   const int lane = threadIdx.x & 63;
+  int64_t v[kSortSub];
+#pragma unroll
   for (int sc = 0; sc < kSortSub; ++sc) {
     const int64_t i = base + sc * 64 + lane;
-    const int bin = i < S ? bin_of(ids[i], E) : E + 1;
+    v[sc] = i < S ? ids[i] : -2;
+  }
+#pragma unroll
+  for (int sc = 0; sc < kSortSub; ++sc) bins[sc] = v[sc] == -2 && base + sc * 64 + lane >= S ? E + 1 : bin_of(v[sc], E);
+}
+
+// Per-wave histogram of the wave's 1024 ids into cnt[0..E] (bin E = sentinels); bin E+1 is not counted.
+__device__ void wave_histogram(const int64_t* ids, int64_t S, int E, int nbits, int64_t base, int* cnt) {
+  const int lane = threadIdx.x & 63;
+  int bins[kSortSub];
+  load_bins(ids, S, E, base, bins);
+#pragma unroll
+  for (int sc = 0; sc < kSortSub; ++sc) {
+    const int bin = bins[sc];
     const uint64_t mask = same_bin(bin, nbits);
     const int leader = 63 - __builtin_clzll(mask);
     if (lane == leader && bin <= E) cnt[bin] += __builtin_popcountll(mask);
@@ -269,9 +284,12 @@ __global__ __launch_bounds__(kSortThreads) void sort_scatter_kernel(const int64_
     }
   }
   __syncthreads();
+  int bins[kSortSub];
+  load_bins(ids, S, E, base, bins);
+#pragma unroll
   for (int sc = 0; sc < kSortSub; ++sc) {
     const int64_t i = base + sc * 64 + lane;
-    const int bin = i < S ? bin_of(ids[i], E) : E + 1;
+    const int bin = bins[sc];
     const uint64_t mask = same_bin(bin, nbits);
     const int leader = 63 - __builtin_clzll(mask);
     const int rank = __builtin_popcountll(mask & ((1ull << lane) - 1ull));
