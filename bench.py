@@ -14,8 +14,8 @@ LoRA r=16, alpha=32 on gate_up and down, bf16.  Data: x, logits ~ N(0,1), W ~ N(
 A ~ Kaiming-uniform U(+-1/sqrt(in)), B ~ N(0,0.01), dY ~ N(0,1), seed 0.
 
 Prints one JSON line: tokens/s (whole job), ms/step, the grouped-product kernel's achieved
-TFLOP/s against the MI355X dense bf16 peak (HIP events around each of its launches inside the
-timed region, on the launch stream), and the CPU baseline: the oracle's float32 per-expert path
+TFLOP/s against the MI355X dense bf16 peak (HIP events around each of its launches over K more steps
+run right after the timed ones, on the launch stream), and the CPU baseline: the oracle's float32 per-expert path
 (the reference's algorithm) on a bounded sample of the same workload on this host's cores.
 """
 
@@ -248,19 +248,8 @@ def main():
         step()
     torch.cuda.synchronize()
 
-    launches = []  # (kind, info, start event, end event)
-
-    def observer(kind, phase, info):
-        if phase == "before":
-            ev = torch.cuda.Event(enable_timing=True)
-            ev.record()
-            launches.append([kind, dict(info), ev, None])
-        else:
-            ev = torch.cuda.Event(enable_timing=True)
-            ev.record()
-            launches[-1][3] = ev
-
-    _grouped.launch_observer = observer
+    # the timed region: K steps with one event on each side (per-launch events would add a few
+    # microseconds of idle GPU per launch and are taken in the pass that follows)
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -270,7 +259,28 @@ def main():
     end.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+
+    # K more steps with HIP events around every grouped-product and reduction launch, on the launch
+    # stream: the kernels' own durations for the roofline
+    launches = []  # (kind, info, start event, end event)
+
+    def observer(kind, phase, info):
+        ev = torch.cuda.Event(enable_timing=True)
+        ev.record()
+        if phase == "before":
+            launches.append([kind, dict(info), ev, None])
+        else:
+            launches[-1][3] = ev
+
+    _grouped.launch_observer = observer
+    istart, iend = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    istart.record()
+    for _ in range(a.steps):
+        step()
+    iend.record()
+    torch.cuda.synchronize()
     _grouped.launch_observer = None
+    ms_instrumented = istart.elapsed_time(iend) / a.steps
 
     ms_per_step = start.elapsed_time(end) / a.steps
     tokens_per_s = T * a.steps / (ms_per_step * a.steps / 1e3)
@@ -310,7 +320,9 @@ def main():
         "roofline": roofline(c, achieved, a.config),
         "kernel_ms_per_step": {"grouped_gemm": round(gemm_ms / a.steps, 4),
                                "grouped_reduce": round(sum(ms for _, ms in red) / a.steps, 4),
-                               "rest": round(ms_per_step - (gemm_ms + sum(ms for _, ms in red)) / a.steps, 4)},
+                               "rest": round(ms_per_step - (gemm_ms + sum(ms for _, ms in red)) / a.steps, 4),
+                               "measured_over": f"{a.steps} steps after the timed ones, HIP events around each "
+                                                f"launch ({ms_instrumented:.4f} ms/step with the events)"},
         "grouped_gemm_ms_by_shape": {k_: round(sum(v) / len(v), 4) for k_, v in per_shape.items()},
         "grouped_reduce_ms_by_shape": {k_: round(sum(v) / len(v), 4) for k_, v in red_shape.items()},
         "wall_s_timed": round(wall, 3),
