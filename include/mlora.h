@@ -39,7 +39,10 @@ enum {
   MLORA_DT_F32 = 1,
   MLORA_DT_F16 = 2,
   MLORA_DT_FP8_E4M3 = 3, /* OCP float8 e4m3fn, torch.float8_e4m3fn */
-  MLORA_DT_NF4 = 4       /* two 4-bit NF4 codes per byte, first element in the high nibble */
+  MLORA_DT_NF4 = 4,      /* two 4-bit NF4 codes per byte, first element in the high nibble */
+  MLORA_DT_NF4_KT = 5    /* NF4 codes of a stack read with k contiguous whose absmax varies along k
+                            (mlora_nf4_transpose's layout): nf4_absmax2 is the fp32 table (E, N/64, K),
+                            nf4_code the 16 codes; the other NF4 arguments are unused */
 };
 
 enum {
@@ -261,6 +264,15 @@ int mlora_nf4_quantize(const void* x, int x_dtype, int64_t n, const float* code,
 int mlora_nf4_dequantize(const uint8_t* packed, const uint8_t* absmax_q, const float* absmax2,
                          const float* offset, const float* code, const float* code2, int64_t n,
                          void* y, int y_dtype, void* stream);
+
+/* An NF4 stack (E, R, C) (blocks of 64 along C, contiguous) read the other way: out_packed (E, C, R/2)
+ * holds its transpose's codes two per byte along R (first in the high nibble), out_absmax (E, C/64, R)
+ * every block's decoded absmax (code2[q] · absmax2 + offset, two roundings).  The grouped product takes
+ * them as MLORA_DT_NF4_KT for the input-gradient pass, where R is k.  R even, C % 64 == 0.  No reference
+ * counterpart: the reference has no NF4 stack path. */
+int mlora_nf4_transpose(const uint8_t* packed, const uint8_t* absmax_q, const float* absmax2, const float* offset,
+                        const float* code2, int64_t E, int64_t R, int64_t C, uint8_t* out_packed, float* out_absmax,
+                        void* stream);
 
 #ifdef __cplusplus
 }

@@ -80,6 +80,22 @@ class Nf4Stack:
         return strides if d is None else strides[d]
 
 
+def _nf4_transposed(stack: Nf4Stack):
+    """(codes (E, C, R/2) uint8, absmax (E, C/64, R) fp32) of an NF4 stack (E, R, C): its transpose's codes
+    packed along R and every block's decoded absmax, for the products that read it with R as k.  Made once by
+    the library's mlora_nf4_transpose and kept on the stack (a frozen stack: made once, reused every step)."""
+    held = getattr(stack, "_mlora_transposed", None)
+    if held is None:
+        E, R, C = stack.shape
+        codes_t = torch.empty((E, C, R // 2), device=stack.device, dtype=torch.uint8)
+        absmax_t = torch.empty((E, C // 64, R), device=stack.device, dtype=torch.float32)
+        call("mlora_nf4_transpose", ptr(stack.packed), ptr(stack.absmax_q), ptr(stack.absmax2), ptr(stack.offset),
+             ptr(stack.code2), E, R, C, ptr(codes_t), ptr(absmax_t), _lib.stream(stack.device))
+        held = (codes_t, absmax_t)
+        stack._mlora_transposed = held
+    return held
+
+
 def _stack_strides(weight, K: int, is_transposed: bool):
     """(N, stride_e, stride_k, stride_n) of a stack addressed as (k, n); src/meepsquared/_grouped.py:264-272."""
     if is_transposed:
@@ -173,7 +189,13 @@ def _launch(x, weight, scale, offsets, is_transposed, adapters, scaling, bias, s
     offsets = offsets.contiguous()
     scale, scale_kind, scale_se, scale_on_k = _scale_args(scale, weight, backward)
     nf4 = (None,) * 5
-    if isinstance(weight, Nf4Stack):
+    if isinstance(weight, Nf4Stack) and w_sk != 1:
+        # read with n contiguous (blocks along n): the stack's transposed codes and absmax table, kept on it
+        codes_t, absmax_t = _nf4_transposed(weight)
+        w_ptr, w_dtype = ptr(codes_t), _lib.DT_NF4_KT
+        w_se, w_sk, w_sn = codes_t.shape[1] * codes_t.shape[2] * 2, 1, codes_t.shape[2] * 2
+        nf4 = (None, ptr(absmax_t), None, None, ptr(weight.code))
+    elif isinstance(weight, Nf4Stack):
         w_ptr, w_dtype = ptr(weight.packed), _lib.DT_NF4
         nf4 = (ptr(weight.absmax_q), ptr(weight.absmax2), ptr(weight.code2), ptr(weight.offset), ptr(weight.code))
     else:

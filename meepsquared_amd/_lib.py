@@ -14,7 +14,7 @@ import torch
 
 LIBRARY = Path(__file__).resolve().parent / "_lib" / "libmlora.so"
 
-DT_BF16, DT_F32, DT_F16, DT_FP8_E4M3, DT_NF4 = 0, 1, 2, 3, 4
+DT_BF16, DT_F32, DT_F16, DT_FP8_E4M3, DT_NF4, DT_NF4_KT = 0, 1, 2, 3, 4, 5
 SCALE_NONE, SCALE_EXPERT, SCALE_ROW = 0, 1, 2
 
 P = c_void_p
@@ -58,6 +58,7 @@ SIGNATURES = {
     "mlora_nf4_workspace_bytes": (c_size_t, [I64]),
     "mlora_nf4_quantize": (c_int, [P, c_int, I64, P, P, P, P, P, P, P, c_size_t, P]),
     "mlora_nf4_dequantize": (c_int, [P, P, P, P, P, P, I64, P, c_int, P]),
+    "mlora_nf4_transpose": (c_int, [P, P, P, P, P, I64, I64, I64, P, P, P]),
 }
 
 

@@ -619,6 +619,10 @@ static int grouped_gemm_impl(const void* x, int64_t ldx, const int64_t* gather, 
     if (other % 8 || w_se % 8 || !aligned(w, 16)) return fail("grouped_gemm: a bf16 stack needs 16-byte aligned rows");
   } else if (w_dtype == MLORA_DT_FP8_E4M3) {
     if (other % 8 || w_se % 8 || !aligned(w, 8)) return fail("grouped_gemm: an fp8 stack needs 8-byte aligned rows");
+  } else if (w_dtype == MLORA_DT_NF4_KT) {
+    if (w_sk != 1 || other % 64 || w_se % 64 || N % 64 || !aligned(w, 16))
+      return fail("grouped_gemm: NF4 codes along k need k contiguous, rows of a multiple of 64 values and N %% 64 == 0");
+    if (!nf4_absmax2 || !nf4_code) return fail("grouped_gemm: NF4 codes along k need their absmax table and code");
   } else if (w_dtype == MLORA_DT_NF4) {
     if (other % 64 || w_se % 64 || !aligned(w, 4))
       return fail("grouped_gemm: an NF4 stack needs rows of a multiple of 64 values");
@@ -669,6 +673,9 @@ static int grouped_gemm_impl(const void* x, int64_t ldx, const int64_t* gather, 
       if (grouped_gemm_dma_takes(g, w_dtype, bkc, scale_k)) return launch_grouped_gemm_dma_q(g, w_dtype, scale_k, s);
       if (scale_k) return bkc ? launch_r<W_FP8, true, true>(g, s) : launch_r<W_FP8, false, true>(g, s);
       return bkc ? launch_r<W_FP8, true, false>(g, s) : launch_r<W_FP8, false, false>(g, s);
+    case MLORA_DT_NF4_KT:
+      if (grouped_gemm_dma_takes(g, w_dtype, bkc, false)) return launch_grouped_gemm_dma_q(g, w_dtype, false, s);
+      return fail("grouped_gemm: NF4 codes along k need a 16-byte aligned stack");
     default:
       if (grouped_gemm_dma_takes(g, w_dtype, bkc, false)) return launch_grouped_gemm_dma_q(g, w_dtype, false, s);
       return bkc ? launch_r<W_NF4, true, false>(g, s) : launch_r<W_NF4, false, false>(g, s);

@@ -178,17 +178,21 @@ __device__ __forceinline__ Item decode(const GemmArgs& p, int64_t item, int nb, 
 // kWFp8K: fp8 with a per-row stack scale that lies along k here (the input-gradient product of a
 // stack with one scale per output row, read through its k-contiguous copy): the stage's BK scales are
 // copied beside the tile and applied in the decode, bf16(e4m3 · s_k), as the register-staged kernel does.
-enum : int { kWBf16 = 0, kWFp8 = 1, kWNf4 = 2, kWFp8K = 3 };
+// kWNf4T: NF4 codes packed along k whose absmax varies with k (the input-gradient product of an NF4
+// stack, read through its transposed copy): the stage's absmax tile, one fp32 per (64 columns, k), is
+// copied beside the codes, and each value decodes as bf16(code[nibble] · absmax) from fp32 codes.
+enum : int { kWBf16 = 0, kWFp8 = 1, kWNf4 = 2, kWFp8K = 3, kWNf4T = 4 };
 template <int WT>
 struct WTile {
   static constexpr bool kFp8 = WT == kWFp8 || WT == kWFp8K;
   static constexpr int RowBytes = WT == kWBf16 ? BK * 2 : kFp8 ? BK : BK / 2;         // one row of the stage
   static constexpr int Chunks = RowBytes / 16;                                         // 16-byte chunks per row
   static constexpr int Bytes = BN * RowBytes;                                          // the tile
-  static constexpr int Elems = Bytes / 2 + (WT == kWFp8K ? BK * 2 : 0);                // bf16 slots of LDS (+ scales)
+  static constexpr int Elems = Bytes / 2 + (WT == kWFp8K ? BK * 2 : WT == kWNf4T ? (BN / 64) * BK * 2 : 0);
+  //                          bf16 slots of LDS (+ the scales along k, or the absmax tile [BN / 64][BK] fp32)
   static constexpr int WI = BN * Chunks / (64 * NW);                                   // copies per wave
   static_assert(BN * Chunks % (64 * NW) == 0, "the stack tile splits evenly over the waves");
-  static_assert(WT != kWFp8K || BK == 64, "one dword copy of 64 lanes carries a stage's scales");
+  static_assert((WT != kWFp8K && WT != kWNf4T) || BK == 64, "one dword copy of 64 lanes carries a row of scales");
 };
 // [n][k] byte tiles of fp8 (4 chunks per row) and NF4 (2): chunk c of row n in slot c ^ g(n)
 template <int WT>
@@ -216,11 +220,13 @@ struct Feed {
   int xk[XI], wk[WI], ak;
   int xd[XI], wd[WI], ad;  // LDS element offset of each instruction's 64 lanes within the slot
   bool a_on;
-  int lane_;
+  int lane_, wave_, n0_;
   int64_t wstep;           // bytes the stack offset advances per k (BKC: 2; else 2 * w_sk)
 
   __device__ __forceinline__ void init(const GemmArgs& p, int n0, int64_t row0, int mrows, int wave, int lane) {
     lane_ = lane;
+    wave_ = wave;
+    n0_ = n0;
 #pragma unroll
     for (int q = 0; q < XI; ++q) {
       const int instr = wave * XI + q, ci = instr * 64 + lane;
@@ -280,9 +286,18 @@ struct Feed {
       dma16(rx, slot + xd[q], xk[q] + k0 < p.K ? xo[q] + (uint32_t)(k0 * 2) : kOob);
 #pragma unroll
     for (int q = 0; q < WI; ++q)
-      dma16(rw, slot + wd[q], wk[q] + k0 < p.K ? wo[q] + (WT == kWNf4 ? (uint32_t)(k0 / 2) : (uint32_t)(k0 * wstep)) : kOob);
+      dma16(rw, slot + wd[q],
+            wk[q] + k0 < p.K ? wo[q] + (WT == kWNf4 || WT == kWNf4T ? (uint32_t)(k0 / 2) : (uint32_t)(k0 * wstep)) : kOob);
     if constexpr (NRB > 0) {
       if (a_on) dma16(ra, slot + ad, ak + k0 < p.K ? ao + (uint32_t)(k0 * 2) : kOob);
+    }
+    if constexpr (WT == kWNf4T) {  // waves 0 .. BN/64 - 1: one row of the absmax tile each
+      if (wave_ < BN / 64) {
+        const int nbg = n0_ / 64 + wave_;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rs, (lds_void*)(slot + BM * BK + WTile<WT>::Bytes / 2 + wave_ * BK * 2), 4,
+            nbg < p.N / 64 && k0 + lane_ < p.K ? (uint32_t)(((int64_t)nbg * p.K + k0 + lane_) * 4) : kOob, 0, 0, 0);
+      }
     }
     if constexpr (WT == kWFp8K) {  // every wave copies the same 64 scales (one dword per lane)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(slot + BM * BK + WTile<WT>::Bytes / 2), 4,
@@ -352,6 +367,21 @@ struct Nf4Pipe {
   int64_t blk[FN];  // the block index of this lane's column j at k = 0, or -1 past N
   uint32_t q[FN];
   float a2[FN];
+  uint32_t pl[4][4];  // kWNf4T: byte p of code[4m .. 4m+3] in pl[p][m]
+  __device__ __forceinline__ void planes(const float* code) {
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const f32x4 c = *(const f32x4*)(code + 4 * m);
+      const uint32_t b0 = __float_as_uint(c[0]), b1 = __float_as_uint(c[1]), b2 = __float_as_uint(c[2]),
+                     b3 = __float_as_uint(c[3]);
+      const uint32_t l01 = __builtin_amdgcn_perm(b1, b0, 0x05010400u), h01 = __builtin_amdgcn_perm(b1, b0, 0x07030602u);
+      const uint32_t l23 = __builtin_amdgcn_perm(b3, b2, 0x05010400u), h23 = __builtin_amdgcn_perm(b3, b2, 0x07030602u);
+      pl[0][m] = __builtin_amdgcn_perm(l23, l01, 0x05040100u);  // bytes 0 of entries 4m .. 4m+3
+      pl[1][m] = __builtin_amdgcn_perm(l23, l01, 0x07060302u);
+      pl[2][m] = __builtin_amdgcn_perm(h23, h01, 0x05040100u);
+      pl[3][m] = __builtin_amdgcn_perm(h23, h01, 0x07060302u);
+    }
+  }
   __device__ __forceinline__ void init(const GemmArgs& p, int e, int n0, int wn, int lane) {
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
@@ -398,6 +428,34 @@ __device__ __forceinline__ void nf4_look(uint32_t g, const uint32_t (&lo)[4], co
   hb = (__builtin_amdgcn_perm(hi[3], hi[2], sel) & m) | (hb & ~m);
 }
 
+// four byte-sized indices (0..15) -> the four fp32 codes they name, from the code's byte planes
+__device__ __forceinline__ void nf4_code4(uint32_t g, const uint32_t (&pl)[4][4], float (&f)[4]) {
+  const uint32_t sel = g & 0x07070707u;
+  const uint32_t m = __builtin_amdgcn_perm(0u, 0u, ((g >> 3) & 0x01010101u) | 0x0C0C0C0Cu);
+  uint32_t t[4];
+#pragma unroll
+  for (int b = 0; b < 4; ++b)
+    t[b] = (__builtin_amdgcn_perm(pl[b][3], pl[b][2], sel) & m) | (__builtin_amdgcn_perm(pl[b][1], pl[b][0], sel) & ~m);
+  // t[b] holds byte b of the four codes; gather each code's four bytes
+  const uint32_t l01 = __builtin_amdgcn_perm(t[1], t[0], 0x05010400u), h01 = __builtin_amdgcn_perm(t[1], t[0], 0x07030602u);
+  const uint32_t l23 = __builtin_amdgcn_perm(t[3], t[2], 0x05010400u), h23 = __builtin_amdgcn_perm(t[3], t[2], 0x07030602u);
+  f[0] = __uint_as_float(__builtin_amdgcn_perm(l23, l01, 0x05040100u));
+  f[1] = __uint_as_float(__builtin_amdgcn_perm(l23, l01, 0x07060302u));
+  f[2] = __uint_as_float(__builtin_amdgcn_perm(h23, h01, 0x05040100u));
+  f[3] = __uint_as_float(__builtin_amdgcn_perm(h23, h01, 0x07060302u));
+}
+
+// eight NF4 codes with one absmax per value (a0: values 0-3, a1: 4-7) -> eight bf16(code · absmax)
+__device__ __forceinline__ bf16x8 nf4t_decode(uint32_t x, const uint32_t (&pl)[4][4], f32x4 a0, f32x4 a1) {
+  float fe[4], fo[4];
+  nf4_code4((x >> 4) & 0x0F0F0F0Fu, pl, fe);  // elements 0, 2, 4, 6
+  nf4_code4(x & 0x0F0F0F0Fu, pl, fo);         // elements 1, 3, 5, 7
+  typedef unsigned u32x4_ __attribute__((ext_vector_type(4)));
+  const u32x4_ w = {pack_bf16x2(fe[0] * a0[0], fo[0] * a0[1]), pack_bf16x2(fe[1] * a0[2], fo[1] * a0[3]),
+                    pack_bf16x2(fe[2] * a1[0], fo[2] * a1[1]), pack_bf16x2(fe[3] * a1[2], fo[3] * a1[3])};
+  return __builtin_bit_cast(bf16x8, w);
+}
+
 // eight NF4 codes (byte j: element 2j in the high nibble, 2j+1 in the low) -> eight bf16
 __device__ __forceinline__ bf16x8 nf4_decode(uint32_t x, const uint32_t (&lo)[4], const uint32_t (&hi)[4]) {
   uint32_t el, eh, ol, oh;
@@ -433,7 +491,13 @@ __device__ __forceinline__ void compute(const GemmArgs& p, const bf16* slot, int
         af[i] = *(const bf16x8*)(as + swz_rk((i * WAVES_M + wm) * 32 + (lane & 31), kk * 2 + (lane >> 5)));
 #pragma unroll
       for (int j = 0; j < FN; ++j) {
-        if constexpr (WT == kWNf4) {
+        if constexpr (WT == kWNf4T) {
+          const int n = (j * WAVES_N + wn) * 32 + (lane & 31);
+          const uint32_t x = *(const uint32_t*)((const uint8_t*)bs + n * (BK / 2) +
+                                                (((kk >> 1) ^ swz_q<WT>(n)) << 4) + (kk & 1) * 8 + 4 * (lane >> 5));
+          const float* a = (const float*)((const uint8_t*)bs + WTile<WT>::Bytes) + (n >> 6) * BK + kk * 16 + 8 * (lane >> 5);
+          bfr[j] = nf4t_decode(x, nf.pl, *(const f32x4*)a, *(const f32x4*)(a + 4));
+        } else if constexpr (WT == kWNf4) {
           // eight codes: byte 8kk/2 + 4(lane/32) of row n (16-byte chunk kk/2)
           const int n = (j * WAVES_N + wn) * 32 + (lane & 31);
           const uint32_t x = *(const uint32_t*)((const uint8_t*)bs + n * (BK / 2) +
@@ -547,6 +611,9 @@ __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_ker
     for (int c = tid0; c < 16 + 256; c += kThreads) code[c] = c < 16 ? p.nf4_code[c] : p.nf4_code2[c - 16];
     off = p.nf4_offset[0];
   }
+  if constexpr (WT == kWNf4T) {
+    for (int c = tid0; c < 16; c += kThreads) code[c] = p.nf4_code[c];
+  }
   build_tile_ends(p, tile_map, sfx, small_last, tid0);
   const int nb = (p.N + BN - 1) / BN;
   // each XCD takes one contiguous eighth of the full tiles' items, then one eighth of the small tiles'
@@ -581,6 +648,8 @@ __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_ker
       const int64_t ebytes = WT == kWBf16 ? p.w_se * 2 : WTile<WT>::kFp8 ? p.w_se : p.w_se / 2;  // one expert's stack
       f.rw = make_rsrc(p.w + (int64_t)e * ebytes, ebytes);
       if constexpr (WT == kWFp8K) f.rs = make_rsrc(p.scale + (int64_t)e * p.scale_se, (int64_t)p.K * 4);
+      if constexpr (WT == kWNf4T)  // the expert's absmax table (N / 64, K)
+        f.rs = make_rsrc(p.nf4_absmax2 + (int64_t)e * (p.N / 64) * p.K, (int64_t)(p.N / 64) * p.K * 4);
     }
     f.ra = f.rx;
     if constexpr (NRB > 0) f.ra = make_rsrc(p.at + (int64_t)e * p.at_se, (int64_t)RP * p.at_sr * 2);
@@ -598,6 +667,7 @@ __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_ker
       for (int j = 0; j < (NRB > 0 ? NRB : 1); ++j) lacc[q][j] = f32x4{};
 
     Nf4Pipe nf;
+    if constexpr (WT == kWNf4T) nf.planes(code);  // (the tile map's barrier published the code book)
     if constexpr (WT == kWNf4) {
       nf.init(p, e, n0, wn, lane);
       nf.load(p, 0);
@@ -752,13 +822,14 @@ __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_ker
 
 static size_t lds_bytes(int E, int WT) {
   const size_t ea = (size_t)((E + 3) & ~3);
-  return ea * sizeof(int) * (E <= kSmallLastE ? 2 : 1) + (WT == kWNf4 ? 272 * 4 : 0);
+  return ea * sizeof(int) * (E <= kSmallLastE ? 2 : 1) + (WT == kWNf4 ? 272 * 4 : WT == kWNf4T ? 16 * 4 : 0);
 }
 static_assert(BM * (kMaxRank + 8) <= SlotSize<4>::kElems &&
                   BN * (kMaxRank + 8) + (STAGES == 4 ? 0 : BN * 3) <= SlotSize<4>::kElems,
               "the epilogue's low, B^T, column-scale and bias tiles must fit in the slots they reuse");
 static_assert(STAGES * SlotSize<4>::kElems * 2 + 4096 * 4 <= 163840, "the slots and the largest tile map fit in LDS");
 static_assert(STAGES * SlotSize<4, kWNf4>::kElems * 2 + 4096 * 4 + 272 * 4 <= 163840, "the same with the NF4 code books");
+static_assert(STAGES * SlotSize<4, kWNf4T>::kElems * 2 + 4096 * 4 + 16 * 4 <= 163840, "the same with the absmax tiles");
 static_assert(STAGES * SlotSize<4>::kElems * 2 + kSmallLastE * 8 <= 163840, "the small-tile counts fit beside the slots");
 static_assert(WTile<kWNf4>::RowBytes * 2 == 64, "an NF4 stage is one block of 64 codes per row");
 
@@ -820,8 +891,9 @@ bool grouped_gemm_dma_takes(const GemmArgs& a, int w_dtype, bool k_contiguous, b
     return a.w_sn % 16 == 0 && a.w_se % 16 == 0 && ((uintptr_t)a.w & 15u) == 0 &&
            (!scale_on_k || (a.scale_kind == MLORA_SCALE_ROW && a.scale_se % 4 == 0 && ((uintptr_t)a.scale & 15u) == 0));
   if (scale_on_k) return false;
-  if (w_dtype == MLORA_DT_NF4)  // rows of whole 64-code blocks (checked by the caller), 16-byte aligned packing
-    return a.w_sn % 64 == 0 && a.w_se % 64 == 0 && ((uintptr_t)a.w & 15u) == 0;
+  if (w_dtype == MLORA_DT_NF4 || w_dtype == MLORA_DT_NF4_KT)  // rows of whole 64-code blocks, 16-byte aligned packing
+    return a.w_sn % 64 == 0 && a.w_se % 64 == 0 && ((uintptr_t)a.w & 15u) == 0 &&
+           (w_dtype == MLORA_DT_NF4 || a.N % 64 == 0);
   return false;
 }
 
@@ -830,6 +902,7 @@ int launch_grouped_gemm_dma_q(const GemmArgs& a, int w_dtype, bool scale_on_k, h
   if (w_dtype == MLORA_DT_FP8_E4M3 && scale_on_k) return dma::launch_r<true, dma::kWFp8K>(a, s);
   if (w_dtype == MLORA_DT_FP8_E4M3) return dma::launch_r<true, dma::kWFp8>(a, s);
   if (w_dtype == MLORA_DT_NF4) return dma::launch_r<true, dma::kWNf4>(a, s);
+  if (w_dtype == MLORA_DT_NF4_KT) return dma::launch_r<true, dma::kWNf4T>(a, s);
   return fail("grouped_gemm: stack dtype %d has no DMA-fed product", w_dtype);
 }
 

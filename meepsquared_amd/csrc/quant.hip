@@ -181,6 +181,40 @@ __global__ __launch_bounds__(256) void nf4_dequant_kernel(const uint8_t* __restr
   }
 }
 
+// The NF4 stack read the other way: from a contiguous stack (E, R, C) (blocks of 64 along C), the codes
+// of its transpose (E, C, R) packed two per byte along R (first in the high nibble), and every block's
+// decoded absmax laid out as (E, C / 64, R): for the input-gradient product, which reads the stack with
+// R as its k.  The values are unchanged: element (e, c, r) decodes as code[nibble] · absmax[e, c/64, r],
+// the same two roundings as nf4_dequant_kernel.
+__global__ __launch_bounds__(256) void nf4_transpose_codes_kernel(const uint8_t* __restrict__ packed, int64_t E,
+                                                                  int64_t R, int64_t C, uint8_t* __restrict__ out) {
+  const int64_t n = E * C * (R / 2);
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t rp = i % (R / 2), ec = i / (R / 2), c = ec % C, e = ec / C;
+    uint32_t nib[2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int64_t el = (e * R + 2 * rp + q) * C + c;
+      const uint32_t byte = packed[el >> 1];
+      nib[q] = (el & 1) ? (byte & 0xFu) : (byte >> 4);
+    }
+    out[i] = (uint8_t)((nib[0] << 4) | nib[1]);
+  }
+}
+
+__global__ __launch_bounds__(256) void nf4_transpose_absmax_kernel(const uint8_t* __restrict__ absmax_q,
+                                                                   const float* __restrict__ absmax2,
+                                                                   const float* __restrict__ offset,
+                                                                   const float* __restrict__ code2, int64_t E,
+                                                                   int64_t R, int64_t C, float* __restrict__ out) {
+  const int64_t cb = C / 64, n = E * cb * R;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i % R, ecb = i / R, b = ecb % cb, e = ecb / cb;
+    const int64_t blk = (e * R + r) * cb + b;
+    out[i] = code2[absmax_q[blk]] * absmax2[blk >> 8] + offset[0];  // two roundings (contraction is off)
+  }
+}
+
 static unsigned grid_of(int64_t n) {
   int64_t g = (n + 255) / 256;
   if (g > 65536) g = 65536;
@@ -267,4 +301,19 @@ extern "C" int mlora_nf4_dequantize(const uint8_t* packed, const uint8_t* absmax
   else
     return fail("nf4_dequantize: dtype %d is not bf16/f32", y_dtype);
   return launch_status("nf4_dequantize");
+}
+
+extern "C" int mlora_nf4_transpose(const uint8_t* packed, const uint8_t* absmax_q, const float* absmax2,
+                                   const float* offset, const float* code2, int64_t E, int64_t R, int64_t C,
+                                   uint8_t* out_packed, float* out_absmax, void* stream) {
+  clear_error();
+  if (E < 1 || R < 2 || R % 2 || C < 64 || C % 64)
+    return fail("nf4_transpose: (E=%lld, R=%lld, C=%lld) needs R even and C a multiple of 64", (long long)E,
+                (long long)R, (long long)C);
+  hipStream_t s = as_stream(stream);
+  hipLaunchKernelGGL(nf4_transpose_codes_kernel, dim3(grid_of(E * C * (R / 2))), dim3(256), 0, s, packed, E, R, C,
+                     out_packed);
+  hipLaunchKernelGGL(nf4_transpose_absmax_kernel, dim3(grid_of(E * (C / 64) * R)), dim3(256), 0, s, absmax_q, absmax2,
+                     offset, code2, E, R, C, out_absmax);
+  return launch_status("nf4_transpose");
 }

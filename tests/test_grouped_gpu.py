@@ -368,3 +368,35 @@ def test_the_input_gradient_through_an_fp8_stack_is_bit_identical_to_its_decoded
         out.backward(dy)
         grads.append(xx.grad)
     assert torch.equal(grads[0], grads[1])
+
+
+@pytest.mark.parametrize("is_transposed", [False, True])
+def test_an_nf4_stack_read_the_other_way_is_bit_identical_to_its_decoded_twin(is_transposed):
+    """The product that reads an NF4 stack with its blocks along n (the input gradient of a stack, or
+    the forward of a transposed one) goes through the stack's transposed codes and absmax table: each
+    value decodes as bf16(code · absmax) with the absmax of its own block, so the input gradient (and,
+    for a transposed stack, the output) is that of the decoded bf16 twin, to the bit."""
+    from meepsquared_amd import _nf4, lora_linear
+
+    torch.manual_seed(8)
+    rows_per_expert = [100, 0, 300, 37]
+    E, K, N, r = len(rows_per_expert), 256, 320, 16
+    offsets = offsets_of(rows_per_expert)
+    w = torch.randn((E, K, N) if is_transposed else (E, N, K), device="cuda") * 0.05
+    stack = _nf4.quantize_stack(w)
+    twin = _nf4.dequantize_stack(stack, torch.bfloat16)
+    if is_transposed:
+        lhs, rhs = torch.randn(E, K, r, device="cuda") * 0.1, torch.randn(E, r, N, device="cuda") * 0.1
+    else:
+        lhs, rhs = torch.randn(E, N, r, device="cuda") * 0.1, torch.randn(E, r, K, device="cuda") * 0.1
+    x = torch.randn(sum(rows_per_expert), K, device="cuda").bfloat16()
+    dy = torch.randn(sum(rows_per_expert), N, device="cuda").bfloat16()
+    res = []
+    for wt in (stack, twin):
+        xx = x.clone().requires_grad_()
+        out = lora_linear(xx, wt, None, offsets, is_transposed, lhs.bfloat16(), rhs.bfloat16(), 2.0)
+        out.backward(dy)
+        res.append((out.detach(), xx.grad))
+    assert torch.equal(res[0][1], res[1][1])
+    if is_transposed:
+        assert torch.equal(res[0][0], res[1][0])
