@@ -180,6 +180,19 @@ int mlora_swiglu(const void* gu, int64_t S, int64_t I, void* act, void* stream);
 /* dgu from dact and gu: dgate = dact · up · silu'(gate), dup = dact · silu(gate). */
 int mlora_swiglu_backward(const void* gu, const void* dact, int64_t S, int64_t I, void* dgu, void* stream);
 
+/* The SwiGLU backward of the layer's down product fused with the combine weights' gradient (no
+ * counterpart function in the reference: it replaces the autograd of src/meepsquared/_moe.py:123-126
+ * (the weighted combine) and of the SwiGLU gate when the down stack has no bias).
+ * g (S, I) bf16 is the down product's input gradient computed WITHOUT the combine weights (the output
+ * gradient read through perm); row p of the expert order has the weight w[perm[p]] (w: T*k, bf16 or
+ * fp32, w_dtype).  Writes dgu (S, 2I) = the SwiGLU backward of (w[perm[p]] · g[p]) and
+ * dw[perm[p]] = <g[p], act[p]> (act recomputed from gu as mlora_swiglu rounds it), which equals
+ * <dout[t], y[p]> for y = the down product without bias.  Rows p >= offsets[E-1] (sentinels): dgu = 0,
+ * dw = 0.  I % 8 == 0. */
+int mlora_swiglu_backward_weighted(const void* gu, const void* g, int64_t S, int64_t I, const void* w, int w_dtype,
+                                   const int64_t* perm, const int32_t* offsets, int E, void* dgu, void* dw,
+                                   void* stream);
+
 /* out[t, :] = sum over j < k of bf16(y[inv[t*k+j], :] · w[t*k+j]) with fp32 accumulation; rows at
  * or past offsets[E-1] (sentinels) contribute nothing.  y (S, H) contiguous, w (T*k) of w_dtype
  * (MLORA_DT_BF16 or MLORA_DT_F32), out (T, H) contiguous.  Replaces _moe.py:123-126. */

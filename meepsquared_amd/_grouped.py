@@ -553,6 +553,81 @@ class _CombinedLoraProduct(torch.autograd.Function):
         return grad_x, dw, None, None, None, None, None, None, None, grad_lhs, grad_rhs, None, None
 
 
+class _SwigluCombinedLoraProduct(torch.autograd.Function):
+    """combine(lora_linear(swiglu(gu), ...), weights) for a down stack without bias
+    (TF:integrations/moe.py:509-520, then src/meepsquared/_moe.py:88-126 for the last product and
+    :123-126).  The backward runs the input-gradient product on dout read through perm WITHOUT the
+    combine weights (g), and one SwiGLU-backward pass applies each row's weight and forms the weights'
+    gradient <dout[t], y[p]> as <g[p], act[p]>: y is neither kept nor read again.  Gradients for gu,
+    the weights and the adapters."""
+
+    @staticmethod
+    def forward(ctx, gu, weights, perm, inv, k, weight, scale, offsets, is_transposed, lhs, rhs, scaling):
+        offsets = offsets.to(torch.int32).contiguous()
+        gu = gu.contiguous()
+        S, I2 = gu.shape
+        act = torch.empty((S, I2 // 2), device=gu.device, dtype=gu.dtype)
+        call("mlora_swiglu", ptr(gu), S, I2 // 2, ptr(act), _lib.stream(gu.device))
+        adapters = _Adapters(lhs, rhs, is_transposed) if lhs is not None else None
+        y, low = _launch(act, weight, scale, offsets, is_transposed, adapters, scaling, None, True)
+        H = y.shape[1]
+        T = inv.numel() // k
+        w = weights.reshape(-1).contiguous()
+        if w.dtype not in (torch.bfloat16, torch.float32):
+            w = w.float()
+        out = torch.empty((T, H), device=y.device, dtype=y.dtype)
+        call("mlora_combine", ptr(y), H, ptr(w), _lib.dtype_code(w.dtype), ptr(inv), T, k, ptr(offsets),
+             offsets.numel(), ptr(out), _lib.stream(y.device))
+        ctx.save_for_backward(gu, act, w, perm, offsets, *((low,) if low is not None else ()))
+        ctx.weight, ctx.adapters, ctx.scale = weight, adapters, scale
+        ctx.is_transposed, ctx.scaling, ctx.k = is_transposed, scaling, k
+        ctx.lhs_dtype = lhs.dtype if lhs is not None else None
+        ctx.wshape, ctx.wdtype = weights.shape, weights.dtype
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        gu, act, w, perm, offsets, *rest = ctx.saved_tensors
+        adapters, weight, k = ctx.adapters, ctx.weight, ctx.k
+        dout = dout.to(torch.bfloat16).contiguous()
+        grad_lhs = grad_rhs = None
+        if adapters is None:
+            g, _ = _launch_gathered(dout, perm, k, weight, ctx.scale, offsets, not ctx.is_transposed, None, 1.0, None,
+                                    backward=True)
+        else:
+            g, low2 = _launch_gathered(dout, perm, k, weight, ctx.scale, offsets, not ctx.is_transposed,
+                                       adapters.swapped(), ctx.scaling, None, backward=True)
+        S, I = g.shape
+        dgu = torch.empty_like(gu)
+        dw = torch.empty_like(w)
+        call("mlora_swiglu_backward_weighted", ptr(gu), ptr(g), S, I, ptr(w), _lib.dtype_code(w.dtype), ptr(perm),
+             ptr(offsets), offsets.numel(), ptr(dgu), ptr(dw), _lib.stream(gu.device))
+        if adapters is not None:
+            low = rest[0]
+            rank = adapters.rank
+            ws = (w, perm)  # row r's weight: w[perm[r]]
+            if ctx.is_transposed:  # A = lhs (in, rank), B = rhs (rank, out)
+                grad_lhs = _reduce(act, low2, offsets, ctx.scaling, row_scale=ws)[:, :, :rank]
+                grad_rhs = _reduce(dout, low, offsets, ctx.scaling, transposed=True, gather=(perm, k),
+                                   row_scale=ws)[:, :rank, :]
+            else:  # A = rhs^T, B = lhs^T
+                grad_rhs = _reduce(act, low2, offsets, ctx.scaling, transposed=True, row_scale=ws)[:, :rank, :]
+                grad_lhs = _reduce(dout, low, offsets, ctx.scaling, gather=(perm, k), row_scale=ws)[:, :, :rank]
+            if ctx.lhs_dtype is not None and ctx.lhs_dtype != torch.bfloat16:
+                grad_lhs, grad_rhs = grad_lhs.to(ctx.lhs_dtype), grad_rhs.to(ctx.lhs_dtype)
+        dw = dw.view(ctx.wshape)
+        if dw.dtype != ctx.wdtype:
+            dw = dw.to(ctx.wdtype)
+        return dgu, dw, None, None, None, None, None, None, None, grad_lhs, grad_rhs, None
+
+
+def swiglu_lora_linear_combined(gu, weights, perm, inv, k, weight, scale, offsets, is_transposed, lhs=None, rhs=None,
+                                scaling: float = 1.0):
+    """combine(lora_linear(swiglu(gu), ...), weights) of the layer's down product (bf16 stack, no bias)."""
+    return _SwigluCombinedLoraProduct.apply(gu, weights, perm, inv, k, weight, scale, offsets, is_transposed, lhs,
+                                            rhs, scaling)
+
+
 def lora_linear_combined(x, weights, perm, inv, k, weight, scale, offsets, is_transposed, lhs=None, rhs=None,
                          scaling: float = 1.0, bias=None):
     """combine(lora_linear(x, ...), weights) of the layer's down product (bf16 stacks), its backward

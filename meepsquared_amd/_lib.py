@@ -46,6 +46,7 @@ SIGNATURES = {
     "mlora_gather_rows_backward": (c_int, [P, I64, P, I64, c_int, P, c_int, P, P]),
     "mlora_swiglu": (c_int, [P, I64, I64, P, P]),
     "mlora_swiglu_backward": (c_int, [P, P, I64, I64, P, P]),
+    "mlora_swiglu_backward_weighted": (c_int, [P, P, I64, I64, P, c_int, P, P, c_int, P, P, P]),
     "mlora_combine": (c_int, [P, I64, P, c_int, P, I64, c_int, P, c_int, P, P]),
     "mlora_combine_backward": (c_int, [P, P, I64, P, c_int, P, I64, c_int, P, c_int, P, P, P]),
     "mlora_transpose": (c_int, [P, I64, I64, I64, I64, I64, I64, P, P]),

@@ -213,6 +213,17 @@ def routed_forward(experts, hidden_states, top_k_index, top_k_weights, factors):
                                                 lhs, rhs, scaling, bias)
     else:
         gate_up = project(_Gather.apply(hidden_states, perm, inv, offsets, k), "gate_up_proj", "gate_up_proj_bias")
+    down_bias = getattr(experts, "has_bias", False) and experts.down_proj_bias is not None
+    if _grouped.gathered_product_fits(experts.down_proj) and not down_bias:
+        # SwiGLU, the down product and the combine as one Function: its backward reads the output
+        # gradient through perm, and the SwiGLU backward applies the combine weights and forms their
+        # gradient (y is not kept)
+        lhs, rhs, scaling = factors.get("down_proj", (None, None, 1.0))
+        result = _grouped.swiglu_lora_linear_combined(gate_up, top_k_weights, perm, inv, k, experts.down_proj,
+                                                      _stack_scale(experts, "down_proj"), offsets,
+                                                      experts.is_transposed, lhs, rhs, scaling)
+        assert result.shape[0] == num_tokens
+        return result.to(hidden_states.dtype)
     act = _SwiGLU.apply(gate_up)
     if _grouped.gathered_product_fits(experts.down_proj):
         # the down product and the combine as one Function: its backward reads the output gradient

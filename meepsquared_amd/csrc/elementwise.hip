@@ -7,6 +7,8 @@
 //   gather   src/meepsquared/_moe.py:80,85-87  selected = h[perm // k], sentinel rows zeroed
 //   SwiGLU   TF:integrations/moe.py:509-520     gate, up = chunk(2); silu(gate) * up
 //   combine  src/meepsquared/_moe.py:123-126   (out * w)[inverse].view(T, k, H).sum(1)
+#include <algorithm>
+
 #include "common.hpp"
 
 namespace mlora {
@@ -120,6 +122,84 @@ __global__ __launch_bounds__(256) void swiglu_backward_kernel(const u32x4* __res
     }
     dgu[r * 2 * Iv + c] = pack8(dg);
     dgu[r * 2 * Iv + Iv + c] = pack8(du);
+  }
+}
+
+// The SwiGLU backward fed by the down product's input gradient g taken WITHOUT the combine weights,
+// with the combine weights' gradient formed on the way.  Row p of the expert order carries the
+// weight w[perm[p]]: dact = w · g, and the weight's gradient <dout[t], y[p]>, with y[p] = act[p]·W_e
+// + scaling · bf16(act[p]·A_e)·B_e (no bias), equals <g[p], act[p]> (g[p] = dout[t]·(W_e^T +
+// scaling · B_e^T A_e^T) is the gradient of that inner product with respect to act[p]); act is
+// recomputed from gu exactly as the forward rounds it, so neither y nor act is read.
+// A block takes `rows` rows (8, fewer for wide rows: their parts fit 32 KB of LDS); its threads stride
+// over the rows' 16-byte vectors (consecutive threads, consecutive vectors), each vector's part of the
+// dot product goes to LDS, and one wave per row sums a row's parts in a fixed order.  Rows from
+// offsets[E-1] on (the sentinels') get zero gradients.
+constexpr int kSwRows = 8;
+constexpr int kSwUnroll = 4;  // vectors per thread loaded together
+
+template <typename TW>
+__global__ __launch_bounds__(256) void swiglu_backward_weighted_kernel(
+    const u32x4* __restrict__ gu, const u32x4* __restrict__ g, int64_t S, int64_t Iv, const TW* __restrict__ w,
+    const int64_t* __restrict__ perm, const int32_t* __restrict__ offsets, int E, u32x4* __restrict__ dgu,
+    TW* __restrict__ dw, int rows) {
+  extern __shared__ float sw_part[];  // rows * Iv vector parts, then the rows' weights
+  float* wrow = sw_part + rows * Iv;
+  const int64_t r0 = (int64_t)blockIdx.x * rows;
+  const int nrows = (int)min((int64_t)rows, S - r0);
+  const int64_t valid = offsets[E - 1];
+  const int tid = threadIdx.x;
+  if (tid < nrows) wrow[tid] = r0 + tid < valid ? load_w(w, perm[r0 + tid]) : 0.f;
+  __syncthreads();
+  const int n = nrows * (int)Iv;
+  for (int i0 = tid; i0 < n; i0 += 256 * kSwUnroll) {  // every load of the kSwUnroll vectors in flight at once
+    u32x4 vg[kSwUnroll], vu[kSwUnroll], vd[kSwUnroll];
+#pragma unroll
+    for (int h = 0; h < kSwUnroll; ++h) {
+      const int i = i0 + 256 * h;
+      if (i < n) {
+        const int rr = i / (int)Iv;
+        const int64_t p = r0 + rr, c = i - rr * Iv;
+        vg[h] = gu[p * 2 * Iv + c];
+        vu[h] = gu[p * 2 * Iv + Iv + c];
+        vd[h] = g[p * Iv + c];
+      }
+    }
+#pragma unroll
+    for (int h = 0; h < kSwUnroll; ++h) {
+      const int i = i0 + 256 * h;
+      if (i >= n) continue;
+      const int rr = i / (int)Iv;
+      const int64_t p = r0 + rr, c = i - rr * Iv;
+      float gg[8], u[8], d[8], dg[8], du[8];
+      unpack8(vg[h], gg);
+      unpack8(vu[h], u);
+      unpack8(vd[h], d);
+      const bool live = p < valid;
+      const float wt = wrow[rr];
+      float dot = 0.f;
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const float sg = sigmoidf_(gg[q]);
+        const float silu = gg[q] * sg;
+        dot += d[q] * round_bf16(silu * u[q]);  // the forward's act value
+        const float dd = wt * d[q];
+        du[q] = live ? dd * silu : 0.f;
+        dg[q] = live ? dd * u[q] * sg * (1.0f + gg[q] * (1.0f - sg)) : 0.f;
+      }
+      dgu[p * 2 * Iv + c] = pack8(dg);
+      dgu[p * 2 * Iv + Iv + c] = pack8(du);
+      sw_part[i] = dot;
+    }
+  }
+  __syncthreads();
+  const int lane = tid & 63;
+  for (int rr = tid >> 6; rr < nrows; rr += 4) {
+    float dot = 0.f;
+    for (int c = lane; c < Iv; c += 64) dot += sw_part[rr * Iv + c];
+    dot = wave_sum(dot);
+    const int64_t p = r0 + rr;
+    if (lane == 0) dw[perm[p]] = (TW)(p < valid ? dot : 0.f);
   }
 }
 
@@ -285,6 +365,30 @@ extern "C" int mlora_swiglu_backward(const void* gu, const void* dact, int64_t S
   return launch_status("swiglu_backward");
 }
 
+extern "C" int mlora_swiglu_backward_weighted(const void* gu, const void* g, int64_t S, int64_t I, const void* w,
+                                              int w_dtype, const int64_t* perm, const int32_t* offsets, int E,
+                                              void* dgu, void* dw, void* stream) {
+  clear_error();
+  if (I % 8) return fail("swiglu_backward_weighted: I=%lld must be a multiple of 8", (long long)I);
+  if (E < 1) return fail("swiglu_backward_weighted: E=%d must be >= 1", E);
+  if (S == 0) return 0;
+  const int64_t Iv = I / 8;
+  if (Iv > 8192) return fail("swiglu_backward_weighted: I=%lld above 65536", (long long)I);
+  const int rows = (int)std::max<int64_t>(1, std::min<int64_t>(kSwRows, 8192 / Iv));
+  if ((S + rows - 1) / rows > 0x7FFFFFFF) return fail("swiglu_backward_weighted: S=%lld too large", (long long)S);
+  const dim3 grid((unsigned)((S + rows - 1) / rows)), block(256);
+  const size_t sh = (size_t)(rows * Iv + rows) * sizeof(float);
+  if (w_dtype == MLORA_DT_F32)
+    hipLaunchKernelGGL(swiglu_backward_weighted_kernel<float>, grid, block, sh, as_stream(stream), (const u32x4*)gu,
+                       (const u32x4*)g, S, Iv, (const float*)w, perm, offsets, E, (u32x4*)dgu, (float*)dw, rows);
+  else if (w_dtype == MLORA_DT_BF16)
+    hipLaunchKernelGGL(swiglu_backward_weighted_kernel<bf16>, grid, block, sh, as_stream(stream), (const u32x4*)gu,
+                       (const u32x4*)g, S, Iv, (const bf16*)w, perm, offsets, E, (u32x4*)dgu, (bf16*)dw, rows);
+  else
+    return fail("swiglu_backward_weighted: weight dtype %d is not bf16/f32", w_dtype);
+  return launch_status("swiglu_backward_weighted");
+}
+
 extern "C" int mlora_combine(const void* y, int64_t H, const void* w, int w_dtype, const int64_t* inv, int64_t T,
                              int k, const int32_t* offsets, int E, void* out, void* stream) {
   clear_error();
@@ -435,6 +539,77 @@ __global__ __launch_bounds__(256) void transpose_vec_kernel(const bf16* __restri
   }
 }
 
+// The narrow-side transpose without LDS: each thread moves one 8 x 16 block (NB: 8 rows of the
+// source by 16 of its narrow columns; else 16 narrow rows by 8 columns) through registers, reading
+// 16-byte vectors along the source's rows and writing 16-byte vectors along the destination's, the
+// pairs of bf16 regrouped by byte permutes.  Consecutive threads take consecutive blocks along the
+// wide side, so both sides' accesses are contiguous across a wave.
+__device__ __forceinline__ uint32_t lo_halves(uint32_t x0, uint32_t x1) { return __builtin_amdgcn_perm(x1, x0, 0x05040100u); }
+__device__ __forceinline__ uint32_t hi_halves(uint32_t x0, uint32_t x1) { return __builtin_amdgcn_perm(x1, x0, 0x07060302u); }
+
+template <bool NB>  // NB: the source's columns (B) are the narrow side
+__global__ __launch_bounds__(64) void transpose_reg_kernel(const bf16* __restrict__ src, int64_t A, int64_t B,
+                                                           int64_t s_e, int64_t s_a, bf16* __restrict__ dst,
+                                                           int64_t items) {
+  const int64_t t = (int64_t)blockIdx.x * 64 + threadIdx.x;
+  if (t >= items) return;
+  if constexpr (NB) {  // rows a0 .. a0+7, columns b0 .. b0+15 -> dst rows b0 .. b0+15, columns a0 .. a0+7
+    const int64_t na = A / 8, nb = B / 16;
+    const int64_t a0 = (t % na) * 8, rest = t / na, b0 = (rest % nb) * 16, e = rest / nb;
+    const bf16* s = src + e * s_e + a0 * s_a + b0;
+    u32x4 r[8][2];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      r[i][0] = *(const u32x4*)(s + i * s_a);
+      r[i][1] = *(const u32x4*)(s + i * s_a + 8);
+    }
+    bf16* d = dst + e * A * B + b0 * A + a0;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      u32x4 o;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint32_t x0 = r[2 * q][j >> 3][(j & 7) >> 1], x1 = r[2 * q + 1][j >> 3][(j & 7) >> 1];
+        o[q] = (j & 1) ? hi_halves(x0, x1) : lo_halves(x0, x1);
+      }
+      *(u32x4*)(d + j * A) = o;
+    }
+  } else {  // rows a0 .. a0+15, columns b0 .. b0+7 -> dst rows b0 .. b0+7, columns a0 .. a0+15
+    const int64_t nbk = B / 8, na = A / 16;
+    const int64_t b0 = (t % nbk) * 8, rest = t / nbk, a0 = (rest % na) * 16, e = rest / na;
+    const bf16* s = src + e * s_e + a0 * s_a + b0;
+    u32x4 r[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) r[i] = *(const u32x4*)(s + i * s_a);
+    bf16* d = dst + e * A * B + b0 * A + a0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        u32x4 o;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t x0 = r[8 * h + 2 * q][j >> 1], x1 = r[8 * h + 2 * q + 1][j >> 1];
+          o[q] = (j & 1) ? hi_halves(x0, x1) : lo_halves(x0, x1);
+        }
+        *(u32x4*)(d + j * A + 8 * h) = o;
+      }
+    }
+  }
+}
+
+template <bool NB>
+static int launch_transpose_reg(const void* src, int64_t E, int64_t A, int64_t B, int64_t s_e, int64_t s_a,
+                                void* dst, void* stream) {
+  const int64_t items = E * (A / (NB ? 8 : 16)) * (B / (NB ? 16 : 8));
+  const int64_t blocks = (items + 63) / 64;
+  if (blocks > 0x7FFFFFFF) return fail("transpose: (E=%lld, A=%lld, B=%lld) exceeds the grid", (long long)E,
+                                       (long long)A, (long long)B);
+  hipLaunchKernelGGL((transpose_reg_kernel<NB>), dim3((unsigned)blocks), dim3(64), 0, as_stream(stream),
+                     (const bf16*)src, A, B, s_e, s_a, (bf16*)dst, items);
+  return launch_status("transpose");
+}
+
 template <int TA, int TB>
 static int launch_transpose_vec(const void* src, int64_t E, int64_t A, int64_t B, int64_t s_e, int64_t s_a,
                                 void* dst, void* stream) {
@@ -470,6 +645,9 @@ extern "C" int mlora_transpose(const void* src, int64_t E, int64_t A, int64_t B,
   if (E == 0 || A == 0 || B == 0) return 0;
   const bool vec = s_b == 1 && A % 8 == 0 && B % 8 == 0 && s_a % 8 == 0 && s_e % 8 == 0 && ((uintptr_t)src & 15u) == 0 &&
                    ((uintptr_t)dst & 15u) == 0;
+  // a narrow side of 16 or 32 (the adapters' rank) with a wide side past it: blocks through registers
+  if (vec && B % 16 == 0 && B <= 32 && A > B) return launch_transpose_reg<true>(src, E, A, B, s_e, s_a, dst, stream);
+  if (vec && A % 16 == 0 && A <= 32 && B > A) return launch_transpose_reg<false>(src, E, A, B, s_e, s_a, dst, stream);
   if (vec && A <= 16 && B > 16) return launch_transpose_vec<16, 256>(src, E, A, B, s_e, s_a, dst, stream);
   if (vec && B <= 16 && A > 16) return launch_transpose_vec<256, 16>(src, E, A, B, s_e, s_a, dst, stream);
   if (vec && A <= 32 && B > 32) return launch_transpose_vec<32, 128>(src, E, A, B, s_e, s_a, dst, stream);

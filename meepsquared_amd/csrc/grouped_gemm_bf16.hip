@@ -600,6 +600,12 @@ __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_ker
 
   bf16* Ls = slot0;  // epilogue: [BM][LP] and [BN][LP], in slots the ring has finished with
   bf16* Lb = slot1;
+  // With one 16-rank block, B_e^T's tile (BN rows of 32 bytes) is copied by DMA at the start of each
+  // item into an LDS region of its own, so the epilogue waits on no load for it.  The two 16-byte
+  // halves of row n sit swapped when bit 2 of n is set: the epilogue's 16-byte reads of 32
+  // consecutive rows then spread over the banks.
+  constexpr bool kPreB = NRB == 1;
+  __shared__ __attribute__((aligned(16))) bf16 lbt[kPreB ? BN * 16 : 8];
 
   // the small-tile counts after the tile map (experts up to kSmallLastE), then the NF4 code book (16)
   // and absmax code book (256)
@@ -673,6 +679,14 @@ __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_ker
       nf.load(p, 0);
     }
     __syncthreads();  // the previous item's epilogue is done with the LDS
+    if constexpr (kPreB) {  // one 16-byte chunk per thread: row tid / 2, half (tid & 1) ^ bit 2 of the row
+      static_assert(BN * 2 == kThreads, "one chunk of the B^T tile per thread");
+      if (p.scaling != 0.f) {
+        const rsrc_t rbt = make_rsrc(p.bt + (int64_t)e * p.bt_se, (int64_t)p.N * p.bt_sn * 2);
+        const int row = tid >> 1, half = (tid & 1) ^ ((row >> 2) & 1), n = n0 + row;
+        dma16(rbt, lbt + (tid >> 6) * 512, n < p.N ? (uint32_t)((n * p.bt_sn + half * 8) * 2) : kOob);
+      }
+    }
 #pragma unroll
     for (int s = 0; s < STAGES - 1; ++s) f.issue(p, slots[s], s);
 
@@ -729,11 +743,13 @@ __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_ker
           for (int v = 0; v < 4; ++v)
             Ls[(rbase + 4 * (lane >> 4) + v) * LP + rb * 16 + (lane & 15)] = (bf16)lacc[q][rb][v];
       }
-      const rsrc_t rbt = make_rsrc(p.bt + (int64_t)e * p.bt_se, (int64_t)p.N * p.bt_sn * 2);
-      for (int c = tid; c < BN * RP / 8; c += kThreads) {
-        const int nn = c / (RP / 8), rc = (c - nn * (RP / 8)) * 8;
-        const int n = n0 + nn;
-        *(u32x4*)(Lb + nn * LP + rc) = ld128(rbt, n < p.N ? (uint32_t)((n * p.bt_sn + rc) * 2) : kOob);
+      if constexpr (!kPreB) {
+        const rsrc_t rbt = make_rsrc(p.bt + (int64_t)e * p.bt_se, (int64_t)p.N * p.bt_sn * 2);
+        for (int c = tid; c < BN * RP / 8; c += kThreads) {
+          const int nn = c / (RP / 8), rc = (c - nn * (RP / 8)) * 8;
+          const int n = n0 + nn;
+          *(u32x4*)(Lb + nn * LP + rc) = ld128(rbt, n < p.N ? (uint32_t)((n * p.bt_sn + rc) * 2) : kOob);
+        }
       }
     }
     __syncthreads();
@@ -764,7 +780,9 @@ __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_ker
 #pragma unroll
             for (int rk = 0; rk < NRB; ++rk) {
               const bf16x8 lf = *(const bf16x8*)(Ls + ((i * WAVES_M + wm) * 32 + (lane & 31)) * LP + rk * 16 + (lane >> 5) * 8);
-              const bf16x8 bfr = *(const bf16x8*)(Lb + ((j * WAVES_N + wn) * 32 + (lane & 31)) * LP + rk * 16 + (lane >> 5) * 8);
+              const int nr = (j * WAVES_N + wn) * 32 + (lane & 31);
+              const bf16x8 bfr = kPreB ? *(const bf16x8*)(lbt + nr * 16 + (((lane >> 5) ^ ((nr >> 2) & 1)) << 3))
+                                       : *(const bf16x8*)(Lb + nr * LP + rk * 16 + (lane >> 5) * 8);
               t = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr, lf, t, 0, 0, 0);
             }
           }
@@ -831,6 +849,8 @@ static_assert(STAGES * SlotSize<4>::kElems * 2 + 4096 * 4 <= 163840, "the slots 
 static_assert(STAGES * SlotSize<4, kWNf4>::kElems * 2 + 4096 * 4 + 272 * 4 <= 163840, "the same with the NF4 code books");
 static_assert(STAGES * SlotSize<4, kWNf4T>::kElems * 2 + 4096 * 4 + 16 * 4 <= 163840, "the same with the absmax tiles");
 static_assert(STAGES * SlotSize<4>::kElems * 2 + kSmallLastE * 8 <= 163840, "the small-tile counts fit beside the slots");
+static_assert(STAGES * SlotSize<1>::kElems * 2 + BN * 16 * 2 + 4096 * 4 <= 163840,
+              "with one rank block: the slots, the B^T tile and the largest tile map fit in LDS");
 static_assert(WTile<kWNf4>::RowBytes * 2 == 64, "an NF4 stage is one block of 64 codes per row");
 
 template <bool BKC, int NRB, int WT>

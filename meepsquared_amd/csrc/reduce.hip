@@ -54,23 +54,33 @@ __global__ __launch_bounds__(256) void grouped_reduce_kernel(const bf16* __restr
 
   u32x4 gv[RPT], lv[RPT];
   float ws[RPT];
+  // the rows a slice reads, fetched one slice ahead so that no load waits on an index load: g's
+  // source row of each of this thread's RPT rows, and the row-scale index of each of its l rows
+  int64_t gsrc[RPT], sidx[RPT];
 #pragma unroll
   for (int q = 0; q < RPT; ++q) ws[q] = 1.f;
+  auto fetch_rows = [&](int64_t row0) {
+#pragma unroll
+    for (int q = 0; q < RPT; ++q) {
+      const int64_t row = row0 + gr + q;
+      gsrc[q] = gather == nullptr || row >= end ? row : (int64_t)((uint32_t)gather[row] / (uint32_t)gk);
+      const int64_t lrow = row0 + lr + q;
+      sidx[q] = row_scale != nullptr && l_owner && lrow < end ? rs_idx[lrow] : 0;
+    }
+  };
   auto load = [&](int64_t row0) {
 #pragma unroll
     for (int q = 0; q < RPT; ++q) {
       const int64_t row = row0 + gr + q;
-      const int64_t src = gather == nullptr || row >= end ? row : gather[row] / gk;  // g's row (gathered rows)
-      gv[q] = (row < end && g_cols) ? *(const u32x4*)(g + src * ldg + n0 + gc) : u32x4{0u, 0u, 0u, 0u};
+      gv[q] = (row < end && g_cols) ? *(const u32x4*)(g + gsrc[q] * ldg + n0 + gc) : u32x4{0u, 0u, 0u, 0u};
       const int64_t lrow = row0 + lr + q;
       if (l_owner) {
         lv[q] = lrow < end ? *(const u32x4*)(l + lrow * ldl + lc) : u32x4{0u, 0u, 0u, 0u};
-        if (row_scale != nullptr && lrow < end) {
-          const int64_t si = rs_idx[lrow];
-          ws[q] = rs_dt == MLORA_DT_F32 ? ((const float*)row_scale)[si] : (float)((const bf16*)row_scale)[si];
-        }
+        if (row_scale != nullptr && lrow < end)
+          ws[q] = rs_dt == MLORA_DT_F32 ? ((const float*)row_scale)[sidx[q]] : (float)((const bf16*)row_scale)[sidx[q]];
       }
     }
+    fetch_rows(row0 + RB_ROWS);
   };
   auto store = [&]() {
     if (row_scale != nullptr && l_owner) {  // l's rows weighted here, after the loads have had the MFMAs to land
@@ -97,7 +107,10 @@ __global__ __launch_bounds__(256) void grouped_reduce_kernel(const bf16* __restr
   f32x4 acc[NRB];
 #pragma unroll
   for (int j = 0; j < NRB; ++j) acc[j] = f32x4{};
-  if (start < end) load(start);
+  if (start < end) {
+    fetch_rows(start);
+    load(start);
+  }
   for (int64_t row0 = start; row0 < end; row0 += RB_ROWS) {
     store();
     __syncthreads();

@@ -11,7 +11,9 @@
 namespace mlora {
 
 // ------------------------------------------------------------------------------------------------
-// top-k softmax: one wave per token, each lane holding the logits e = lane + 64*i
+// top-k softmax: L lanes per token (64 / L tokens per wave), lane g of a token holding the logits
+// e = g + L*i, i < PL.  Every reduction over a token's lanes is a butterfly of DPP moves (quad
+// permutations, then the half-row and row mirrors), so the k selection rounds never touch LDS.
 // ------------------------------------------------------------------------------------------------
 
 template <typename T>
@@ -23,7 +25,7 @@ __device__ __forceinline__ float load_logit<bf16>(const bf16* p) { return (float
 template <>
 __device__ __forceinline__ float load_logit<_Float16>(const _Float16* p) { return (float)*p; }
 
-// A key whose unsigned order is (value descending, then index ascending) under max.
+// A key whose unsigned order is (value descending, then index ascending) under max; never 0.
 __device__ __forceinline__ uint64_t rank_key(float v, int idx) {
   uint32_t b = __float_as_uint(v + 0.0f);  // -0 and +0 are one value
   uint32_t ord = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
@@ -35,60 +37,111 @@ __device__ __forceinline__ float key_value(uint64_t key) {
   return __uint_as_float(b);
 }
 
-constexpr int kTopkMaxPerLane = 16;  // E <= 1024
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+}
+// The value of this lane's partner at step S of a butterfly over aligned groups of 2^(S+1) lanes:
+// lane ^ 1, lane ^ 2 (quad permutations), then the mirror image within 8 and within 16 lanes (each
+// pairs the two halves of the group reduced so far), then lane ^ 16 and lane ^ 32.
+template <int S>
+__device__ __forceinline__ uint32_t bfly(uint32_t v) {
+  if constexpr (S == 0) return dpp_u32<0xB1>(v);        // quad_perm [1, 0, 3, 2]
+  else if constexpr (S == 1) return dpp_u32<0x4E>(v);   // quad_perm [2, 3, 0, 1]
+  else if constexpr (S == 2) return dpp_u32<0x141>(v);  // row_half_mirror
+  else if constexpr (S == 3) return dpp_u32<0x140>(v);  // row_mirror
+  else return (uint32_t)__shfl_xor((int)v, S == 4 ? 16 : 32, kWave);
+}
+// Reductions over a token's L lanes; every lane of the group ends with the same value (each step
+// combines two equal-shaped partial results with a commutative operation).
+template <int L, int S = 0>
+__device__ __forceinline__ float group_max(float v) {
+  if constexpr ((1 << S) >= L) return v;
+  else return group_max<L, S + 1>(fmaxf(v, __uint_as_float(bfly<S>(__float_as_uint(v)))));
+}
+template <int L, int S = 0>
+__device__ __forceinline__ float group_sum(float v) {
+  if constexpr ((1 << S) >= L) return v;
+  else return group_sum<L, S + 1>(v + __uint_as_float(bfly<S>(__float_as_uint(v))));
+}
+template <int L, int S = 0>
+__device__ __forceinline__ uint64_t group_max_key(uint64_t v) {
+  if constexpr ((1 << S) >= L) {
+    return v;
+  } else {
+    const uint64_t w = ((uint64_t)bfly<S>((uint32_t)(v >> 32)) << 32) | bfly<S>((uint32_t)v);
+    return group_max_key<L, S + 1>(w > v ? w : v);
+  }
+}
 
-template <typename TL, typename TW, int PL>  // PL: logits per lane, ceil(E / 64)
+constexpr int kTopkMaxE = 1024;
+
+template <typename TL, typename TW, int L, int PL>
 __global__ __launch_bounds__(256) void topk_softmax_kernel(const TL* __restrict__ logits, int64_t ld, int64_t T,
                                                            int E, int k, int renorm, int64_t* __restrict__ out_idx,
                                                            TW* __restrict__ out_w) {
-  const int lane = threadIdx.x & 63;
-  const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (t >= T) return;
-  const TL* row = logits + t * ld;
+  constexpr int G = kWave / L;  // tokens per wave
+  const int lane = threadIdx.x & 63, gl = lane & (L - 1);
+  const int64_t t0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * G;
+  if (t0 >= T) return;  // whole waves only: the reductions need every lane of a live wave
+  const int64_t t = t0 + lane / L;
+  const bool live = t < T;
+  const TL* row = logits + (live ? t : 0) * ld;
   float v[PL];
   float m = -INFINITY;
 #pragma unroll
   for (int i = 0; i < PL; ++i) {
-    const int e = lane + 64 * i;
-    v[i] = (e < E) ? load_logit(row + e) : -INFINITY;
+    const int e = gl + L * i;
+    v[i] = (live && e < E) ? load_logit(row + e) : -INFINITY;
     m = fmaxf(m, v[i]);
   }
-  m = wave_max(m);
+  m = group_max<L>(m);
   float z = 0.f;
+  uint64_t key[PL];
 #pragma unroll
   for (int i = 0; i < PL; ++i) {
-    const int e = lane + 64 * i;
+    const int e = gl + L * i;
     if (e < E) z += expf(v[i] - m);
+    key[i] = e < E ? rank_key(v[i], e) : 0;  // 0: absent or already taken
   }
-  z = wave_sum(z);
+  z = group_sum<L>(z);
 
-  uint32_t taken = 0;
-  float sel_sum = 0.f, my_p = 0.f;
-  int my_idx = 0;
+  // round j: the largest key left over the token's lanes; lane j % L keeps it in its slot j / L
+  float sel_sum = 0.f, sp[PL];
+  int si[PL];
+#pragma unroll
+  for (int s = 0; s < PL; ++s) {
+    sp[s] = 0.f;
+    si[s] = 0;
+  }
   for (int j = 0; j < k; ++j) {
     uint64_t best = 0;
 #pragma unroll
-    for (int i = 0; i < PL; ++i) {
-      const int e = lane + 64 * i;
-      if (e < E && !((taken >> i) & 1u)) {
-        uint64_t key = rank_key(v[i], e);
-        best = key > best ? key : best;
-      }
-    }
-    best = wave_max_u64(best);
+    for (int i = 0; i < PL; ++i) best = key[i] > best ? key[i] : best;
+    best = group_max_key<L>(best);
+#pragma unroll
+    for (int i = 0; i < PL; ++i) key[i] = key[i] == best ? 0 : key[i];
     const int idx = (int)(0xFFFFFFFFu - (uint32_t)best);
-    if ((idx & 63) == lane) taken |= 1u << (idx >> 6);
     const float p = expf(key_value(best) - m) / z;
     sel_sum += p;
-    if (lane == j) {
-      my_p = p;
-      my_idx = idx;
+    if (gl == (j & (L - 1))) {
+#pragma unroll
+      for (int s = 0; s < PL; ++s)
+        if (s == j / L) {
+          sp[s] = p;
+          si[s] = idx;
+        }
     }
   }
-  if (lane < k) {
-    const float w = renorm ? my_p / sel_sum : my_p;
-    out_idx[t * k + lane] = my_idx;
-    out_w[t * k + lane] = (TW)w;
+  if (live) {
+#pragma unroll
+    for (int s = 0; s < PL; ++s) {
+      const int j = s * L + gl;
+      if (j < k) {
+        out_idx[t * k + j] = si[s];
+        out_w[t * k + j] = (TW)(renorm ? sp[s] / sel_sum : sp[s]);
+      }
+    }
   }
 }
 
@@ -168,12 +221,12 @@ __global__ __launch_bounds__(1024) void tile_map_kernel(const int32_t* __restric
 }
 
 // ------------------------------------------------------------------------------------------------
-// counting sort: histogram per block, a scan over (bin, block), a stable scatter
+// counting sort: one wave per chunk of 256 ids.  A histogram per chunk, one block that turns the
+// (chunk, bin) counts into each chunk's first position per bin, then a stable scatter per chunk.
 // ------------------------------------------------------------------------------------------------
-constexpr int kSortThreads = 256;
-constexpr int kSortWaves = kSortThreads / 64;
-constexpr int kSortSub = 16;                                 // sub-chunks of 64 per wave
-constexpr int kSortChunk = kSortThreads * kSortSub;           // ids per block
+constexpr int kSortSub = 4;                  // sub-chunks of 64 ids per chunk
+constexpr int kSortChunk = kWave * kSortSub;  // ids per chunk (one wave, one workgroup)
+constexpr int kScanThreads = 1024;
 
 __device__ __forceinline__ int bin_of(int64_t id, int E) { return (id >= 0 && id < E) ? (int)id : E; }
 
@@ -188,104 +241,147 @@ __device__ __forceinline__ uint64_t same_bin(int bin, int nbits) {
   return m;
 }
 
-// The bins of this lane's ids in the wave's 1024 (all loaded before any is used: one memory round
-// trip, not one per sub-chunk); bin E+1 marks lanes past the end of the ids.
-__device__ __forceinline__ void load_bins(const int64_t* ids, int64_t S, int E, int64_t base, int (&bins)[kSortSub]) {
+// The bins of this lane's ids in chunk `c` (all loaded before any is used); bin E+1 marks lanes past
+// the end of the ids.
+__device__ __forceinline__ void load_bins(const int64_t* ids, int64_t S, int E, int64_t c, int (&bins)[kSortSub]) {
   const int lane = threadIdx.x & 63;
+  const int64_t base = c * kSortChunk;
   int64_t v[kSortSub];
 #pragma unroll
   for (int sc = 0; sc < kSortSub; ++sc) {
     const int64_t i = base + sc * 64 + lane;
-    v[sc] = i < S ? ids[i] : -2;
+    v[sc] = i < S ? ids[i] : 0;
   }
 #pragma unroll
-  for (int sc = 0; sc < kSortSub; ++sc) bins[sc] = v[sc] == -2 && base + sc * 64 + lane >= S ? E + 1 : bin_of(v[sc], E);
+  for (int sc = 0; sc < kSortSub; ++sc) bins[sc] = base + sc * 64 + lane >= S ? E + 1 : bin_of(v[sc], E);
 }
 
-// Per-wave histogram of the wave's 1024 ids into cnt[0..E] (bin E = sentinels); bin E+1 is not counted.
-__device__ void wave_histogram(const int64_t* ids, int64_t S, int E, int nbits, int64_t base, int* cnt) {
-  const int lane = threadIdx.x & 63;
+// ws[c][e] = how many ids of chunk c fall in bin e (bin E: the sentinels)
+__global__ __launch_bounds__(kWave) void sort_hist_kernel(const int64_t* __restrict__ ids, int64_t S, int E,
+                                                          int32_t* __restrict__ ws) {
+  extern __shared__ int cnt[];  // E + 1
+  const int lane = threadIdx.x;
+  for (int e = lane; e <= E; e += kWave) cnt[e] = 0;
+  __syncthreads();
   int bins[kSortSub];
-  load_bins(ids, S, E, base, bins);
+  load_bins(ids, S, E, blockIdx.x, bins);
 #pragma unroll
-  for (int sc = 0; sc < kSortSub; ++sc) {
-    const int bin = bins[sc];
-    const uint64_t mask = same_bin(bin, nbits);
-    const int leader = 63 - __builtin_clzll(mask);
-    if (lane == leader && bin <= E) cnt[bin] += __builtin_popcountll(mask);
-    __builtin_amdgcn_wave_barrier();
-  }
+  for (int sc = 0; sc < kSortSub; ++sc)
+    if (bins[sc] <= E) atomicAdd(&cnt[bins[sc]], 1);
+  __syncthreads();
+  for (int e = lane; e <= E; e += kWave) ws[(int64_t)blockIdx.x * (E + 1) + e] = cnt[e];
 }
 
-__global__ __launch_bounds__(kSortThreads) void sort_hist_kernel(const int64_t* __restrict__ ids, int64_t S, int E,
-                                                                 int nbits, int32_t* __restrict__ ws) {
-  extern __shared__ int sh[];  // kSortWaves x (E+1)
-  const int w = threadIdx.x >> 6;
-  for (int i = threadIdx.x; i < kSortWaves * (E + 1); i += kSortThreads) sh[i] = 0;
-  __syncthreads();
-  const int64_t base = (int64_t)blockIdx.x * kSortChunk + (int64_t)w * (kSortChunk / kSortWaves);
-  wave_histogram(ids, S, E, nbits, base, sh + w * (E + 1));
-  __syncthreads();
-  for (int e = threadIdx.x; e <= E; e += kSortThreads) {
-    int s = 0;
-    for (int ww = 0; ww < kSortWaves; ++ww) s += sh[ww * (E + 1) + e];
-    ws[(int64_t)blockIdx.x * (E + 1) + e] = s;
-  }
+constexpr int kScanBatch = 16;  // chunks per load batch
+constexpr int kScanGroups = 4;  // 64-bin groups loaded together
+
+// The NP ranges of chunks the scan splits each bin's column into: as many as fit 48 KB of LDS.
+__host__ __device__ inline int scan_ranges(int E) {
+  const int G = (E + 1 + 63) / 64;
+  int np = 16;
+  while (np > 1 && np * G * 64 * (int)sizeof(int) > 48 * 1024) np >>= 1;
+  return np;
 }
 
-// One block: per bin, the exclusive sum over blocks (in place in ws), then the bins' starts added;
-// offsets and, when asked, the tile map.
-__global__ __launch_bounds__(1024) void sort_scan_kernel(int32_t* __restrict__ ws, int nblk, int E,
-                                                         int32_t* __restrict__ offsets, int bm, int32_t* tile_expert,
-                                                         int32_t* tile_row, int32_t* tiles, int64_t max_tiles) {
+// The counts ws[c][g*64 + l] of chunks cb .. cb + kScanBatch - 1 (those below c1) for the groups
+// g0 .. g0 + kScanGroups - 1 (those up to bin E): kScanGroups x kScanBatch loads in flight at once.
+__device__ __forceinline__ void scan_load(const int32_t* ws, int E, int l, int g0, int cb, int c1,
+                                          int (&val)[kScanGroups][kScanBatch]) {
+#pragma unroll
+  for (int gi = 0; gi < kScanGroups; ++gi)
+#pragma unroll
+    for (int u = 0; u < kScanBatch; ++u) {
+      const int e = (g0 + gi) * 64 + l, c = cb + u;
+      val[gi][u] = c < c1 && e <= E ? ws[(int64_t)c * (E + 1) + e] : 0;
+    }
+}
+
+// One block: start[e] = the first row of bin e (an exclusive scan of the bins' totals), offsets, then
+// every ws[c][e] replaced by the first row of chunk c's ids of bin e.  Thread (w, l), w < NP, handles
+// bin g*64 + l of every 64-bin group g over the w-th of NP ranges of chunks (pass 1: its sums; pass 2:
+// the running first rows written back); the ranges' sums are scanned down each bin's column in LDS.
+__global__ __launch_bounds__(kScanThreads) void sort_scan_kernel(int32_t* __restrict__ ws, int nch, int E,
+                                                                 int32_t* __restrict__ offsets, int bm,
+                                                                 int32_t* tile_expert, int32_t* tile_row,
+                                                                 int32_t* tiles, int64_t max_tiles) {
   extern __shared__ int sh[];
   int* start = sh;              // E + 2: per-bin totals, scanned into starts
   int* tstart = sh + (E + 2);   // E + 1
   int* tmp = tstart + (E + 1);  // 17
-  for (int e = threadIdx.x; e <= E; e += blockDim.x) {
-    int s = 0;
-    for (int b = 0; b < nblk; ++b) {
-      const int c = ws[(int64_t)b * (E + 1) + e];
-      ws[(int64_t)b * (E + 1) + e] = s;
-      s += c;
+  int* part = tmp + 17;         // [G][NP][64]: each range's count of each bin, then its first row
+  const int NP = scan_ranges(E), G = (E + 1 + 63) / 64;
+  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63;
+  const int per = (nch + NP - 1) / NP;
+  const int c0 = w < NP ? min(w * per, nch) : nch, c1 = w < NP ? min(c0 + per, nch) : nch;
+  for (int g0 = 0; g0 < G; g0 += kScanGroups) {
+    int sum[kScanGroups] = {};
+    for (int cb = c0; cb < c1; cb += kScanBatch) {
+      int val[kScanGroups][kScanBatch];
+      scan_load(ws, E, l, g0, cb, c1, val);
+#pragma unroll
+      for (int gi = 0; gi < kScanGroups; ++gi)
+#pragma unroll
+        for (int u = 0; u < kScanBatch; ++u) sum[gi] += val[gi][u];
     }
-    start[e] = s;
+    if (w < NP) {
+#pragma unroll
+      for (int gi = 0; gi < kScanGroups; ++gi)
+        if (g0 + gi < G) part[((g0 + gi) * NP + w) * 64 + l] = sum[gi];
+    }
+  }
+  __syncthreads();
+  for (int e = tid; e <= E; e += kScanThreads) {
+    const int g = e >> 6, ll = e & 63;
+    int tot = 0;
+    for (int q = 0; q < NP; ++q) tot += part[(g * NP + q) * 64 + ll];
+    start[e] = tot;
   }
   __syncthreads();
   block_exclusive_scan(start, E + 1, tmp);  // start[e] = first row of bin e; start[E] = offsets[E-1]
-  for (int e = threadIdx.x; e <= E; e += blockDim.x) {
-    const int st = start[e];
-    for (int b = 0; b < nblk; ++b) ws[(int64_t)b * (E + 1) + e] += st;
-    if (e > 0) offsets[e - 1] = st;
+  for (int e = tid + 1; e <= E; e += kScanThreads) offsets[e - 1] = start[e];
+  for (int e = tid; e <= E; e += kScanThreads) {  // each bin's column: the first row of each range
+    const int g = e >> 6, ll = e & 63;
+    int run = start[e];
+    for (int q = 0; q < NP; ++q) {
+      const int c = part[(g * NP + q) * 64 + ll];
+      part[(g * NP + q) * 64 + ll] = run;
+      run += c;
+    }
+  }
+  __syncthreads();
+  for (int g0 = 0; g0 < G; g0 += kScanGroups) {
+    int run[kScanGroups];
+#pragma unroll
+    for (int gi = 0; gi < kScanGroups; ++gi) run[gi] = w < NP && g0 + gi < G ? part[((g0 + gi) * NP + w) * 64 + l] : 0;
+    for (int cb = c0; cb < c1; cb += kScanBatch) {
+      int val[kScanGroups][kScanBatch];
+      scan_load(ws, E, l, g0, cb, c1, val);
+#pragma unroll
+      for (int gi = 0; gi < kScanGroups; ++gi)
+#pragma unroll
+        for (int u = 0; u < kScanBatch; ++u) {
+          const int e = (g0 + gi) * 64 + l, c = cb + u;
+          if (c < c1 && e <= E) ws[(int64_t)c * (E + 1) + e] = run[gi];
+          run[gi] += val[gi][u];
+        }
+    }
   }
   __syncthreads();
   if (tile_expert != nullptr) write_tile_map(start, tstart, tmp, E, bm, tile_expert, tile_row, tiles, max_tiles);
 }
 
-__global__ __launch_bounds__(kSortThreads) void sort_scatter_kernel(const int64_t* __restrict__ ids, int64_t S, int E,
-                                                                    int nbits, const int32_t* __restrict__ ws,
-                                                                    int64_t* __restrict__ perm,
-                                                                    int64_t* __restrict__ inv) {
-  extern __shared__ int sh[];  // kSortWaves x (E+1)
-  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  for (int i = threadIdx.x; i < kSortWaves * (E + 1); i += kSortThreads) sh[i] = 0;
-  __syncthreads();
-  const int64_t base = (int64_t)blockIdx.x * kSortChunk + (int64_t)w * (kSortChunk / kSortWaves);
-  int* cnt = sh + w * (E + 1);
-  wave_histogram(ids, S, E, nbits, base, cnt);
-  __syncthreads();
-  // each wave's first position per bin: the block's base, then the earlier waves' counts
-  for (int e = threadIdx.x; e <= E; e += kSortThreads) {
-    int run = ws[(int64_t)blockIdx.x * (E + 1) + e];
-    for (int ww = 0; ww < kSortWaves; ++ww) {
-      const int c = sh[ww * (E + 1) + e];
-      sh[ww * (E + 1) + e] = run;
-      run += c;
-    }
-  }
-  __syncthreads();
+// Chunk c's ids in order: each id's position is its bin's next free row, taken a sub-chunk of 64 at
+// a time (lanes of one bin in lane order), so equal ids keep their input order.
+__global__ __launch_bounds__(kWave) void sort_scatter_kernel(const int64_t* __restrict__ ids, int64_t S, int E,
+                                                             int nbits, const int32_t* __restrict__ ws,
+                                                             int64_t* __restrict__ perm, int64_t* __restrict__ inv) {
+  extern __shared__ int cnt[];  // E + 1: the next row of each bin
+  const int lane = threadIdx.x;
   int bins[kSortSub];
-  load_bins(ids, S, E, base, bins);
+  load_bins(ids, S, E, blockIdx.x, bins);
+  for (int e = lane; e <= E; e += kWave) cnt[e] = ws[(int64_t)blockIdx.x * (E + 1) + e];
+  __syncthreads();
+  const int64_t base = (int64_t)blockIdx.x * kSortChunk;
 #pragma unroll
   for (int sc = 0; sc < kSortSub; ++sc) {
     const int64_t i = base + sc * 64 + lane;
@@ -314,22 +410,27 @@ extern "C" int mlora_route_topk(const void* logits, int logits_dtype, int64_t ld
                                 int renorm, int64_t* out_idx, void* out_w, int w_dtype, void* stream) {
   clear_error();
   if (T < 0) return fail("route_topk: T=%lld is negative", (long long)T);
-  if (E < 1 || E > 64 * kTopkMaxPerLane) return fail("route_topk: E=%d outside [1, %d]", E, 64 * kTopkMaxPerLane);
+  if (E < 1 || E > kTopkMaxE) return fail("route_topk: E=%d outside [1, %d]", E, kTopkMaxE);
   if (k < 1 || k > E || k > 64) return fail("route_topk: k=%d outside [1, min(E=%d, 64)]", k, E);
   if (ld_logits < E) return fail("route_topk: ld_logits=%lld < E=%d", (long long)ld_logits, E);
   if (T == 0) return 0;
-  const dim3 grid((unsigned)((T + 3) / 4)), block(256);
   hipStream_t s = as_stream(stream);
-#define MLORA_TOPK_PL(TL, TW, PL)                                                                        \
-  hipLaunchKernelGGL((topk_softmax_kernel<TL, TW, PL>), grid, block, 0, s, (const TL*)logits, ld_logits, T, E, \
-                     k, renorm, out_idx, (TW*)out_w)
+  // lanes per token L and logits per lane PL: 8 logits per lane up to E = 512
+  const int L = E <= 32 ? 4 : E <= 64 ? 8 : E <= 128 ? 16 : E <= 256 ? 32 : 64;
+  const int64_t waves = (T + kWave / L - 1) / (kWave / L);
+  const dim3 grid((unsigned)((waves + 3) / 4)), block(256);
+#define MLORA_TOPK_LP(TL, TW, L_, PL)                                                                      \
+  hipLaunchKernelGGL((topk_softmax_kernel<TL, TW, L_, PL>), grid, block, 0, s, (const TL*)logits, ld_logits, T, \
+                     E, k, renorm, out_idx, (TW*)out_w)
 #define MLORA_TOPK(TL, TW)                                                                                     \
   do {                                                                                                         \
-    if (E <= 64) MLORA_TOPK_PL(TL, TW, 1);                                                                     \
-    else if (E <= 128) MLORA_TOPK_PL(TL, TW, 2);                                                               \
-    else if (E <= 256) MLORA_TOPK_PL(TL, TW, 4);                                                               \
-    else if (E <= 512) MLORA_TOPK_PL(TL, TW, 8);                                                               \
-    else MLORA_TOPK_PL(TL, TW, kTopkMaxPerLane);                                                               \
+    if (E <= 8) MLORA_TOPK_LP(TL, TW, 4, 2);                                                                   \
+    else if (E <= 32) MLORA_TOPK_LP(TL, TW, 4, 8);                                                             \
+    else if (E <= 64) MLORA_TOPK_LP(TL, TW, 8, 8);                                                             \
+    else if (E <= 128) MLORA_TOPK_LP(TL, TW, 16, 8);                                                           \
+    else if (E <= 256) MLORA_TOPK_LP(TL, TW, 32, 8);                                                           \
+    else if (E <= 512) MLORA_TOPK_LP(TL, TW, 64, 8);                                                           \
+    else MLORA_TOPK_LP(TL, TW, 64, 16);                                                                        \
   } while (0)
   if (w_dtype != MLORA_DT_BF16 && w_dtype != MLORA_DT_F32) return fail("route_topk: w_dtype %d is not bf16/f32", w_dtype);
   const bool wf = w_dtype == MLORA_DT_F32;
@@ -340,13 +441,13 @@ extern "C" int mlora_route_topk(const void* logits, int logits_dtype, int64_t ld
     default: return fail("route_topk: logits dtype %d is not bf16/f16/f32", logits_dtype);
   }
 #undef MLORA_TOPK
-#undef MLORA_TOPK_PL
+#undef MLORA_TOPK_LP
   return launch_status("route_topk");
 }
 
 extern "C" size_t mlora_route_sort_workspace_bytes(int64_t S, int E) {
-  const int64_t nblk = S > 0 ? (S + kSortChunk - 1) / kSortChunk : 1;
-  return (size_t)nblk * (size_t)(E + 1) * sizeof(int32_t);
+  const int64_t nch = S > 0 ? (S + kSortChunk - 1) / kSortChunk : 1;
+  return (size_t)nch * (size_t)(E + 1) * sizeof(int32_t);
 }
 
 extern "C" int mlora_route_sort(const int64_t* ids, int64_t S, int E, int64_t* perm, int64_t* inv, int32_t* offsets,
@@ -361,21 +462,20 @@ extern "C" int mlora_route_sort(const int64_t* ids, int64_t S, int E, int64_t* p
   if (workspace == nullptr || workspace_bytes < need)
     return fail("route_sort: workspace of %zu bytes, %zu needed", workspace_bytes, need);
   hipStream_t s = as_stream(stream);
-  const int nblk = (int)(S > 0 ? (S + kSortChunk - 1) / kSortChunk : 0);
+  const int nch = (int)(S > 0 ? (S + kSortChunk - 1) / kSortChunk : 0);
   int32_t* ws = (int32_t*)workspace;
   const int nbits = nbits_for(E);
-  const size_t sh_waves = (size_t)kSortWaves * (E + 1) * sizeof(int);
-  if (nblk > 0) {
-    hipLaunchKernelGGL(sort_hist_kernel, dim3(nblk), dim3(kSortThreads), sh_waves, s, ids, S, E, nbits, ws);
+  const size_t sh_bins = (size_t)(E + 1) * sizeof(int);
+  if (nch > 0) {
+    hipLaunchKernelGGL(sort_hist_kernel, dim3(nch), dim3(kWave), sh_bins, s, ids, S, E, ws);
     if (int rc = launch_status("route_sort/hist")) return rc;
   }
-  const size_t sh_scan = (size_t)((E + 2) + (E + 1) + 17) * sizeof(int);
-  hipLaunchKernelGGL(sort_scan_kernel, dim3(1), dim3(1024), sh_scan, s, ws, nblk, E, offsets, block_m, tile_expert,
-                     tile_row, tiles, max_tiles);
+  const size_t sh_scan = (size_t)((E + 2) + (E + 1) + 17 + ((E + 1 + 63) / 64) * scan_ranges(E) * 64) * sizeof(int);
+  hipLaunchKernelGGL(sort_scan_kernel, dim3(1), dim3(kScanThreads), sh_scan, s, ws, nch, E, offsets, block_m,
+                     tile_expert, tile_row, tiles, max_tiles);
   if (int rc = launch_status("route_sort/scan")) return rc;
-  if (nblk > 0) {
-    hipLaunchKernelGGL(sort_scatter_kernel, dim3(nblk), dim3(kSortThreads), sh_waves, s, ids, S, E, nbits, ws, perm,
-                       inv);
+  if (nch > 0) {
+    hipLaunchKernelGGL(sort_scatter_kernel, dim3(nch), dim3(kWave), sh_bins, s, ids, S, E, nbits, ws, perm, inv);
     if (int rc = launch_status("route_sort/scatter")) return rc;
   }
   return 0;

@@ -17,15 +17,18 @@ def swiglu(gate_up):
 
 
 def routed_forward(hidden, top_k_index, top_k_weights, gate_up, down, factors, num_experts, is_transposed=False,
-                   scales=None, dtype=torch.float32):
+                   scales=None, dtype=torch.float32, biases=None):
     """The layer forward — src/meepsquared/_moe.py:70-126 with reference_lora per projection.
 
     factors: {"gate_up_proj": (lhs, rhs, s), "down_proj": (lhs, rhs, s)}; scales: the same names to
     fp8 scales (or absent).  Computed in `dtype` (float32 by default), differentiable in hidden,
-    top_k_weights and the factors.  Sentinel ids (>= num_experts) contribute nothing.
+    top_k_weights and the factors.  Sentinel ids (>= num_experts) contribute nothing.  biases: the
+    same names to (experts, out) bias stacks (or absent), added per expert as the reference's
+    lora_linear adds `bias` (src/meepsquared/_grouped.py:408-417).
     Pinned by: a per-token brute-force loop over its k experts (tests/test_oracle.py).
     """
     scales = scales or {}
+    biases = biases or {}
     T, k = top_k_index.shape
     ids = top_k_index.reshape(-1)
     perm, _, offsets = routing.sort_by_expert(ids.cpu().numpy(), num_experts)
@@ -37,7 +40,7 @@ def routed_forward(hidden, top_k_index, top_k_weights, gate_up, down, factors, n
     def project(x, name, weight):
         lhs, rhs, s = factors.get(name, (None, None, 1.0))
         return grouped.reference_lora(x, weight, scales.get(name), offsets, is_transposed, lhs, rhs, s,
-                                      out_dtype=dtype)
+                                      biases.get(name), out_dtype=dtype)
 
     act = swiglu(project(selected, "gate_up_proj", gate_up))
     out = project(act, "down_proj", down)

@@ -58,7 +58,8 @@ def test_a_refusal_reports_its_reason_without_a_gpu():
     rc = _lib.lib.mlora_grouped_gemm(*args)
     assert rc != 0
     assert b"E=0" in _lib.lib.mlora_last_error()
-    assert _lib.lib.mlora_route_sort_workspace_bytes(65536, 128) == 16 * 129 * 4
+    # one (E + 1)-bin count per chunk of 256 ids
+    assert _lib.lib.mlora_route_sort_workspace_bytes(65536, 128) == 256 * 129 * 4
 
 
 def test_a_mismatched_stack_is_refused():

@@ -28,7 +28,7 @@ def make_layer(T, H, I, E, k, r, alpha, seed=0, is_transposed=False, zipf=0.0):
 
 
 def run_layer(T, H, I, E, k, r, alpha, is_transposed=False, sentinel_frac=0.0, seed=0, fp8=None, nf4=False,
-              zipf=0.0):
+              zipf=0.0, bias=False):
     from meepsquared_amd import Experts, _fp8, _nf4, routed_forward, topk_softmax
 
     h, logits, gu, dn, f = make_layer(T, H, I, E, k, r, alpha, seed, is_transposed, zipf)
@@ -47,7 +47,13 @@ def run_layer(T, H, I, E, k, r, alpha, is_transposed=False, sentinel_frac=0.0, s
         scales = {"gate_up_proj": s1, "down_proj": s2}
     if nf4:
         gub, dnb = _nf4.quantize_stack(gub), _nf4.quantize_stack(dnb)
-    experts = Experts(gub, dnb, is_transposed, scales.get("gate_up_proj"), scales.get("down_proj"))
+    biases = {}
+    if bias:  # bias stacks (experts, out), as gpt-oss's experts hold them
+        bg = torch.Generator().manual_seed(seed + 7)
+        biases = {"gate_up_proj": (torch.randn(E, 2 * I, generator=bg) * 0.1).to(dev, torch.bfloat16),
+                  "down_proj": (torch.randn(E, H, generator=bg) * 0.1).to(dev, torch.bfloat16)}
+    experts = Experts(gub, dnb, is_transposed, scales.get("gate_up_proj"), scales.get("down_proj"),
+                      biases.get("gate_up_proj"), biases.get("down_proj"))
     fb = {n: (a.to(dev, torch.bfloat16).requires_grad_(), b.to(dev, torch.bfloat16).requires_grad_(), s)
           for n, (a, b, s) in f.items()}
     out = routed_forward(experts, hb, idx, w, fb)
@@ -65,7 +71,8 @@ def run_layer(T, H, I, E, k, r, alpha, is_transposed=False, sentinel_frac=0.0, s
     else:
         gu32, dn32 = gub.float(), dnb.float()
     f32 = {n: (a.detach().float().requires_grad_(), b.detach().float().requires_grad_(), s) for n, (a, b, s) in fb.items()}
-    o32 = ref_moe.routed_forward(h32, idx, w32, gu32, dn32, f32, E, is_transposed, scales=scales)
+    o32 = ref_moe.routed_forward(h32, idx, w32, gu32, dn32, f32, E, is_transposed, scales=scales,
+                                 biases={n: b.float() for n, b in biases.items()})
     o32.backward(dy.float())
     want = {"out": o32.detach(), "dh": h32.grad, "dw": w32.grad}
     for n, (a, b, _) in f32.items():
@@ -77,6 +84,14 @@ def run_layer(T, H, I, E, k, r, alpha, is_transposed=False, sentinel_frac=0.0, s
 def test_config0_layer_forward_and_backward(is_transposed):
     # BASELINE config 0 shapes: T=512, H=256, I=512, E=8, top-2, r=8, alpha=16
     got, want = run_layer(512, 256, 512, 8, 2, 8, 16, is_transposed)
+    for name in want:
+        assert rel(got[name], want[name]) < 1e-2, (name, rel(got[name], want[name]))
+
+
+@pytest.mark.parametrize("is_transposed", [False, True])
+def test_layer_with_bias_stacks(is_transposed):
+    # experts with a bias per output (gpt-oss): the down product keeps y for the combine weights' gradient
+    got, want = run_layer(300, 128, 64, 8, 2, 16, 32, is_transposed, sentinel_frac=0.05, seed=6, bias=True)
     for name in want:
         assert rel(got[name], want[name]) < 1e-2, (name, rel(got[name], want[name]))
 
@@ -158,5 +173,56 @@ def test_the_combined_down_product_matches_the_product_then_the_combine(is_trans
     assert rel(got[1], want[1]) < 1e-2  # the weights' gradient: the same dot products, summed in another order
     valid = int(offsets[-1])  # rows past it are sentinels' and take no gradient
     assert rel(got[2][:valid], want[2][:valid]) < 1e-2
+    for i in (3, 4):
+        assert rel(got[i], want[i]) < 1e-2
+
+
+@pytest.mark.parametrize("is_transposed", [False, True])
+@pytest.mark.parametrize("weights_dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("I", [128, 8704])  # 8704: rows wider than 8 fit in the SwiGLU backward's LDS
+def test_swiglu_and_the_combined_down_product_match_the_composed_steps(is_transposed, weights_dtype, I):
+    """swiglu_lora_linear_combined (SwiGLU, the down product and the combine in one Function, the weights'
+    gradient formed in the SwiGLU backward as <g, act>) against SwiGLU, lora_linear and the combine
+    composed: the same output bits; the gradients within bf16 rounding of each other (<g, act> and
+    <dout, y> are the same sum taken over other roundings; the weights enter the SwiGLU backward in
+    fp32 instead of through bf16(w · dout))."""
+    from meepsquared_amd import _grouped, _moe, sort_by_expert, topk_softmax
+
+    torch.manual_seed(12)
+    T, H, E, k, r = 300, 192, 8, 2, 16
+    dev = "cuda"
+    logits = torch.randn(T, E, device=dev)
+    w, idx = topk_softmax(logits.to(torch.bfloat16), k, weights_dtype=weights_dtype)
+    idx = torch.where(torch.rand(idx.shape, device=dev) < 0.05, torch.full_like(idx, E), idx)  # a few sentinels
+    perm, inv, offsets = sort_by_expert(idx, E)
+    gu = torch.randn(T * k, 2 * I, device=dev).bfloat16()
+    down = (torch.randn((E, I, H) if is_transposed else (E, H, I), device=dev) * 0.05).bfloat16()
+    if is_transposed:
+        lhs, rhs = torch.randn(E, I, r, device=dev) * 0.1, torch.randn(E, r, H, device=dev) * 0.1
+    else:
+        lhs, rhs = torch.randn(E, H, r, device=dev) * 0.1, torch.randn(E, r, I, device=dev) * 0.1
+    dres = torch.randn(T, H, device=dev).bfloat16()
+
+    def run(fused):
+        g = gu.clone().requires_grad_()
+        ww = w.detach().clone().requires_grad_()
+        l_, r_ = lhs.bfloat16().requires_grad_(), rhs.bfloat16().requires_grad_()
+        if fused:
+            out = _grouped.swiglu_lora_linear_combined(g, ww, perm, inv, k, down, None, offsets, is_transposed, l_,
+                                                       r_, 2.0)
+        else:
+            y = _grouped.lora_linear(_moe._SwiGLU.apply(g), down, None, offsets, is_transposed, l_, r_, 2.0)
+            out = _moe._Combine.apply(y, ww, inv, offsets, k)
+        out.backward(dres)
+        return out.detach(), ww.grad, g.grad, l_.grad, r_.grad
+
+    got, want = run(True), run(False)
+    assert torch.equal(got[0], want[0])
+    assert rel(got[1], want[1]) < 1e-2
+    sentinel = (idx.reshape(-1) == E).reshape(got[1].shape)
+    assert torch.all(got[1][sentinel] == 0)
+    valid = int(offsets[-1])  # rows past it are sentinels' and take no gradient
+    assert rel(got[2][:valid], want[2][:valid]) < 1e-2
+    assert torch.all(got[2][valid:] == 0)
     for i in (3, 4):
         assert rel(got[i], want[i]) < 1e-2
