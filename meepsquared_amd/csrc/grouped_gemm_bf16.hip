@@ -278,20 +278,31 @@ struct Feed {
   }
 
   // the copies of stage kt into `slot` (past the end of K they read zeros, so the count per stage
-  // never changes)
+  // never changes), in three parts that the K loop spreads over a stage's MFMAs: the x tile, the
+  // stack tile (with its scales), the A^T tile
   __device__ __forceinline__ void issue(const GemmArgs& p, bf16* slot, int kt) const {
+    issue_part<0>(p, slot, kt);
+    issue_part<1>(p, slot, kt);
+    issue_part<2>(p, slot, kt);
+  }
+  template <int PART>
+  __device__ __forceinline__ void issue_part(const GemmArgs& p, bf16* slot, int kt) const {
     const int k0 = kt * BK;
+    if constexpr (PART == 0) {
 #pragma unroll
-    for (int q = 0; q < XI; ++q)
-      dma16(rx, slot + xd[q], xk[q] + k0 < p.K ? xo[q] + (uint32_t)(k0 * 2) : kOob);
+      for (int q = 0; q < XI; ++q)
+        dma16(rx, slot + xd[q], xk[q] + k0 < p.K ? xo[q] + (uint32_t)(k0 * 2) : kOob);
+    }
+    if constexpr (PART == 1) {
 #pragma unroll
-    for (int q = 0; q < WI; ++q)
-      dma16(rw, slot + wd[q],
-            wk[q] + k0 < p.K ? wo[q] + (WT == kWNf4 || WT == kWNf4T ? (uint32_t)(k0 / 2) : (uint32_t)(k0 * wstep)) : kOob);
-    if constexpr (NRB > 0) {
+      for (int q = 0; q < WI; ++q)
+        dma16(rw, slot + wd[q],
+              wk[q] + k0 < p.K ? wo[q] + (WT == kWNf4 || WT == kWNf4T ? (uint32_t)(k0 / 2) : (uint32_t)(k0 * wstep)) : kOob);
+    }
+    if constexpr (PART == 2 && NRB > 0) {
       if (a_on) dma16(ra, slot + ad, ak + k0 < p.K ? ao + (uint32_t)(k0 * 2) : kOob);
     }
-    if constexpr (WT == kWNf4T) {  // waves 0 .. BN/64 - 1: one row of the absmax tile each
+    if constexpr (PART == 1 && WT == kWNf4T) {  // waves 0 .. BN/64 - 1: one row of the absmax tile each
       if (wave_ < BN / 64) {
         const int nbg = n0_ / 64 + wave_;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
@@ -299,7 +310,7 @@ struct Feed {
             nbg < p.N / 64 && k0 + lane_ < p.K ? (uint32_t)(((int64_t)nbg * p.K + k0 + lane_) * 4) : kOob, 0, 0, 0);
       }
     }
-    if constexpr (WT == kWFp8K) {  // every wave copies the same 64 scales (one dword per lane)
+    if constexpr (PART == 1 && WT == kWFp8K) {  // every wave copies the same 64 scales (one dword per lane)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(slot + BM * BK + WTile<WT>::Bytes / 2), 4,
                                                k0 + lane_ < p.K ? (uint32_t)((k0 + lane_) * 4) : kOob, 0, 0, 0);
     }
@@ -470,10 +481,13 @@ __device__ __forceinline__ bf16x8 nf4_decode(uint32_t x, const uint32_t (&lo)[4]
 }
 
 // The MFMAs of one stage held in `slot` for a wave with AM live row blocks.
+// The copies of the next stage (into nslot) are issued in three parts after the first MFMA steps:
+// issued back to back they fill the texture unit's queues and hold the wave in front of its MFMAs.
 template <int AM, bool BKC, int NRB, int WT>
 __device__ __forceinline__ void compute(const GemmArgs& p, const bf16* slot, int lane, int wm, int wn,
                                         f32x16 (&acc)[FM][FN], f32x4 (&lacc)[kLS][NRB > 0 ? NRB : 1],
-                                        Nf4Pipe& nf, const float* code, float off, int kt) {
+                                        Nf4Pipe& nf, const float* code, float off, int kt,
+                                        const Feed<BKC, NRB, WT>& f, bf16* nslot, int nkt) {
   const bf16* as = slot;
   const bf16* bs = slot + BM * BK;
   uint32_t tlo[WT == kWNf4 ? FN : 1][4], thi[WT == kWNf4 ? FN : 1][4];
@@ -482,6 +496,7 @@ __device__ __forceinline__ void compute(const GemmArgs& p, const bf16* slot, int
     for (int j = 0; j < FN; ++j) nf4_table(code, nf4_absmax(code[16 + nf.q[j]], nf.a2[j], off), tlo[j], thi[j]);
     nf.load(p, kt + 1);
   }
+  if constexpr (AM == 0) f.issue(p, nslot, nkt);
   if constexpr (AM > 0) {
 #pragma unroll
     for (int kk = 0; kk < BK / 16; ++kk) {
@@ -512,6 +527,12 @@ __device__ __forceinline__ void compute(const GemmArgs& p, const bf16* slot, int
 #pragma unroll
         for (int j = 0; j < FN; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[j], af[i], acc[i][j], 0, 0, 0);
+      constexpr int last = BK / 16 - 1;
+      if (kk <= 2 || kk == last) __builtin_amdgcn_sched_barrier(0);
+      if (kk == 0) f.template issue_part<0>(p, nslot, nkt);
+      if (kk == 1 || (kk == last && last < 1)) f.template issue_part<1>(p, nslot, nkt);
+      if (kk == 2 || (kk == last && last < 2)) f.template issue_part<2>(p, nslot, nkt);
+      if (kk <= 2 || kk == last) __builtin_amdgcn_sched_barrier(0);
     }
     if constexpr (NRB > 0) {
       const bf16* aa = slot + BM * BK + WTile<WT>::Elems;
@@ -545,8 +566,8 @@ __device__ __forceinline__ void stage(const GemmArgs& p, const Feed<BKC, NRB, WT
                                       float off) {
   wait_vm<Feed<BKC, NRB, WT>::PS * (STAGES - 2)>();  // stages kt+1, kt+2 may stay in flight
   stage_barrier();
-  f.issue(p, slots[(S + STAGES - 1) % STAGES], kt + STAGES - 1);
-  compute<AM, BKC, NRB, WT>(p, slots[S], lane, wm, wn, acc, lacc, nf, code, off, kt);
+  compute<AM, BKC, NRB, WT>(p, slots[S], lane, wm, wn, acc, lacc, nf, code, off, kt, f,
+                            slots[(S + STAGES - 1) % STAGES], kt + STAGES - 1);
 }
 
 // The K loop of one item, unrolled by the ring depth so every slot index is a constant.
