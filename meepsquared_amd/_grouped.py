@@ -343,6 +343,8 @@ def _reduce(g: torch.Tensor, low: torch.Tensor, offsets: torch.Tensor, scaling: 
     else:
         out = torch.empty((experts, N, R), device=g.device, dtype=torch.bfloat16)
         o_se, o_sn, o_sr = out.stride(0), out.stride(1), out.stride(2)
+    if rows == 0:  # a sum over no rows (an empty gather or scale index has no device pointer to pass)
+        return out.zero_()
     info = {"rows": rows, "N": N, "R": R, "gathered": gather is not None, "scaled": row_scale is not None}
     if launch_observer is not None:
         launch_observer("grouped_reduce", "before", info)

@@ -701,8 +701,8 @@ __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_ker
     }
     __syncthreads();  // the previous item's epilogue is done with the LDS
     if constexpr (kPreB) {  // one 16-byte chunk per thread: row tid / 2, half (tid & 1) ^ bit 2 of the row
-      static_assert(BN * 2 == kThreads, "one chunk of the B^T tile per thread");
-      if (p.scaling != 0.f) {
+      static_assert(BN * 2 <= kThreads, "one chunk of the B^T tile per thread");
+      if (p.scaling != 0.f && tid < BN * 2) {
         const rsrc_t rbt = make_rsrc(p.bt + (int64_t)e * p.bt_se, (int64_t)p.N * p.bt_sn * 2);
         const int row = tid >> 1, half = (tid & 1) ^ ((row >> 2) & 1), n = n0 + row;
         dma16(rbt, lbt + (tid >> 6) * 512, n < p.N ? (uint32_t)((n * p.bt_sn + half * 8) * 2) : kOob);

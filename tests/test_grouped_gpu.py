@@ -159,6 +159,25 @@ def test_an_nf4_stack_computes_what_its_dequantised_twin_computes(is_transposed)
         assert rel(a, b) < Q_TOL, (name, rel(a, b))
 
 
+@pytest.mark.parametrize("is_transposed", [False, True])
+def test_an_empty_input_gives_an_empty_output_and_zero_adapter_gradients(is_transposed):
+    """rows == 0 (src/meepsquared/_grouped.py:325-326): an empty output, an empty input gradient, and
+    adapter gradients of zero (no row contributes)."""
+    from meepsquared_amd import lora_linear
+
+    E, K, N, r = 3, 64, 96, 16
+    x = torch.zeros(0, K, device="cuda", dtype=torch.bfloat16, requires_grad=True)
+    offsets = torch.zeros(E, device="cuda", dtype=torch.int32)
+    shape = (E, K, N) if is_transposed else (E, N, K)
+    weight = torch.randn(shape, device="cuda", dtype=torch.bfloat16)
+    lhs, rhs = adapters(E, K, N, r, is_transposed)
+    out = lora_linear(x, weight, None, offsets, is_transposed, lhs, rhs, 2.0)
+    assert out.shape == (0, N)
+    out.backward(torch.zeros_like(out))
+    assert x.grad.shape == (0, K)
+    assert torch.count_nonzero(lhs.grad) == 0 and torch.count_nonzero(rhs.grad) == 0
+
+
 def test_the_product_is_deterministic():
     from meepsquared_amd import lora_linear
 

@@ -96,6 +96,36 @@ def test_layer_with_bias_stacks(is_transposed):
         assert rel(got[name], want[name]) < 1e-2, (name, rel(got[name], want[name]))
 
 
+def test_layer_with_every_id_a_sentinel():
+    # every (token, slot) routed to another rank (ids >= E): the layer adds nothing, and every
+    # gradient is zero
+    got, want = run_layer(64, 128, 64, 8, 2, 16, 32, sentinel_frac=1.0)
+    for name in want:
+        assert torch.count_nonzero(got[name]) == 0, name
+        assert want[name] is None or torch.count_nonzero(want[name]) == 0, name  # (None: no path to it)
+
+
+def test_layer_on_no_tokens():
+    from meepsquared_amd import Experts, routed_forward, topk_softmax
+
+    E, H, I, k, r = 8, 128, 64, 2, 16
+    h = torch.zeros(0, H, device="cuda", dtype=torch.bfloat16, requires_grad=True)
+    w, idx = topk_softmax(torch.zeros(0, E, device="cuda", dtype=torch.bfloat16), k)
+    assert w.shape == (0, k) and idx.shape == (0, k)
+    gu = torch.randn(E, 2 * I, H, device="cuda").bfloat16()
+    dn = torch.randn(E, H, I, device="cuda").bfloat16()
+    f = {"gate_up_proj": (torch.zeros(E, 2 * I, r, device="cuda").bfloat16().requires_grad_(),
+                          torch.zeros(E, r, H, device="cuda").bfloat16().requires_grad_(), 2.0),
+         "down_proj": (torch.zeros(E, H, r, device="cuda").bfloat16().requires_grad_(),
+                       torch.zeros(E, r, I, device="cuda").bfloat16().requires_grad_(), 2.0)}
+    out = routed_forward(Experts(gu, dn), h, idx, w.requires_grad_(), f)
+    assert out.shape == (0, H)
+    out.backward(torch.zeros_like(out))
+    assert h.grad.shape == (0, H)
+    for a, b, _ in f.values():
+        assert torch.count_nonzero(a.grad) == 0 and torch.count_nonzero(b.grad) == 0
+
+
 def test_layer_with_sentinel_ids():
     got, want = run_layer(300, 128, 64, 8, 2, 16, 32, sentinel_frac=0.1)
     for name in want:
