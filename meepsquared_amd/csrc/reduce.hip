@@ -37,7 +37,11 @@ __global__ __launch_bounds__(256) void grouped_reduce_kernel(const bf16* __restr
   constexpr int R = NRB * 16;
   __shared__ __attribute__((aligned(16))) bf16 Gs[RB_N * RP_];  // [n][row]
   __shared__ __attribute__((aligned(16))) bf16 Ls[R * RP_];     // [r][row]
-  const int e = blockIdx.x, n0 = blockIdx.y * RB_N;
+  // gathered rows: consecutive workgroups take consecutive column blocks of one expert, so the rows
+  // they read at once are whole rows of the source (4 % faster at config 1); the expert's own rows:
+  // consecutive workgroups take consecutive experts (5 % faster)
+  const int e = gather != nullptr ? blockIdx.y : blockIdx.x;
+  const int n0 = (gather != nullptr ? blockIdx.x : blockIdx.y) * RB_N;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   // the expert's rows, clamped into [0, rows]
   const int64_t start = e == 0 ? 0 : min(max((int64_t)offsets[e - 1], (int64_t)0), rows);
@@ -154,7 +158,8 @@ static int grouped_reduce_impl(const void* g, int64_t ldg, const int64_t* gather
     return fail("grouped_reduce: g needs N (%d) and its row stride (%lld) multiples of 8, 16-byte aligned", N, (long long)ldg);
   if (R < 16 || R > 64 || R % 16) return fail("grouped_reduce: R=%d must be 16, 32, 48 or 64", R);
   if (ldl < R || ldl % 8 || ((uintptr_t)l & 15u)) return fail("grouped_reduce: l needs 16-byte aligned rows of >= R values");
-  const dim3 grid((unsigned)E, (unsigned)((N + RB_N - 1) / RB_N)), block(256);
+  const unsigned nblk = (unsigned)((N + RB_N - 1) / RB_N);
+  const dim3 grid(gather != nullptr ? nblk : (unsigned)E, gather != nullptr ? (unsigned)E : nblk), block(256);
   hipStream_t s = as_stream(stream);
 #define MLORA_RED(NRB)                                                                                               \
   hipLaunchKernelGGL(grouped_reduce_kernel<NRB>, grid, block, 0, s, (const bf16*)g, ldg, gather, gk, row_scale, rs_dt,   \
