@@ -62,6 +62,8 @@ __device__ __forceinline__ void for_slots(int k, F&& f) {
   }
 }
 
+// One token per workgroup: the token's k row indices are workgroup-uniform (scalar loads), its
+// threads stride over the row's 16-byte vectors.
 template <int KT>
 __global__ __launch_bounds__(256) void gather_rows_backward_kernel(const u32x4* __restrict__ dsel, int64_t Hv,
                                                                    const int64_t* __restrict__ inv, int64_t T, int k,
@@ -69,20 +71,36 @@ __global__ __launch_bounds__(256) void gather_rows_backward_kernel(const u32x4* 
                                                                    u32x4* __restrict__ dh) {
   if constexpr (KT > 0) k = KT;
   const int64_t valid = offsets[E - 1];
-  const int64_t total = T * Hv;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t t = i / Hv, c = i - t * Hv;
+  const int64_t t = blockIdx.x;
+  for (int64_t c = threadIdx.x; c < Hv; c += blockDim.x) {
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for_slots<KT>(k, [&](int j) {
-      const int64_t p = inv[t * k + j];
-      if (p < valid) {
-        float f[8];
-        unpack8(dsel[p * Hv + c], f);
+    if constexpr (KT > 0) {  // every slot's row loaded before any is added (a sentinel's reads row 0, unused)
+      u32x4 v[KT];
 #pragma unroll
-        for (int q = 0; q < 8; ++q) acc[q] += f[q];
+      for (int j = 0; j < KT; ++j) {
+        const int64_t p = inv[t * KT + j];
+        v[j] = dsel[(p < valid ? p : 0) * Hv + c];
       }
-    });
-    dh[i] = pack8(acc);
+#pragma unroll
+      for (int j = 0; j < KT; ++j) {
+        float f[8];
+        unpack8(v[j], f);
+        const bool ok = inv[t * KT + j] < valid;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) acc[q] += ok ? f[q] : 0.f;
+      }
+    } else {
+      for (int j = 0; j < k; ++j) {
+        const int64_t p = inv[t * k + j];
+        if (p < valid) {
+          float f[8];
+          unpack8(dsel[p * Hv + c], f);
+#pragma unroll
+          for (int q = 0; q < 8; ++q) acc[q] += f[q];
+        }
+      }
+    }
+    dh[t * Hv + c] = pack8(acc);
   }
 }
 
@@ -212,24 +230,38 @@ __global__ __launch_bounds__(256) void combine_kernel(const u32x4* __restrict__ 
   constexpr bool kBf16Weights = sizeof(TW) == 2;
   if constexpr (KT > 0) k = KT;
   const int64_t valid = offsets[E - 1];
-  const int64_t total = T * Hv;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t t = i / Hv, c = i - t * Hv;
+  const int64_t t = blockIdx.x;  // one token per workgroup (row indices and weights workgroup-uniform)
+  for (int64_t c = threadIdx.x; c < Hv; c += blockDim.x) {
+    const int64_t i = t * Hv + c;
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for_slots<KT>(k, [&](int j) {
-      const int64_t p = inv[t * k + j];
-      if (p < valid) {
-        const float wt = load_w(w, t * k + j);
-        float f[8];
-        unpack8(y[p * Hv + c], f);
+    auto add = [&](const u32x4& v, float wt) {
+      float f[8];
+      unpack8(v, f);
 #pragma unroll
-        for (int q = 0; q < 8; ++q) {
-          // with bf16 weights the reference's product is a bf16 tensor; with fp32 weights it is fp32
-          const float prod = f[q] * wt;
-          acc[q] += kBf16Weights ? round_bf16(prod) : prod;
-        }
+      for (int q = 0; q < 8; ++q) {
+        // with bf16 weights the reference's product is a bf16 tensor; with fp32 weights it is fp32
+        const float prod = f[q] * wt;
+        acc[q] += kBf16Weights ? round_bf16(prod) : prod;
       }
-    });
+    };
+    if constexpr (KT > 0) {  // every slot's row and weight loaded before any is added (a sentinel reads row 0)
+      u32x4 v[KT];
+      float wt[KT];
+#pragma unroll
+      for (int j = 0; j < KT; ++j) {
+        const int64_t p = inv[t * KT + j];
+        v[j] = y[(p < valid ? p : 0) * Hv + c];
+        wt[j] = load_w(w, t * KT + j);
+      }
+#pragma unroll
+      for (int j = 0; j < KT; ++j)
+        if (inv[t * KT + j] < valid) add(v[j], wt[j]);
+    } else {
+      for (int j = 0; j < k; ++j) {
+        const int64_t p = inv[t * k + j];
+        if (p < valid) add(y[p * Hv + c], load_w(w, t * k + j));
+      }
+    }
     out[i] = pack8(acc);
   }
 }
@@ -331,7 +363,8 @@ extern "C" int mlora_gather_rows_backward(const void* dsel, int64_t H, const int
   if (H % 8) return fail("gather_rows_backward: H=%lld must be a multiple of 8", (long long)H);
   if (k < 1 || E < 1) return fail("gather_rows_backward: k=%d, E=%d must be >= 1", k, E);
   if (T == 0) return 0;
-  const dim3 g(grid_for(T * (H / 8))), b(256);
+  if (T > 0x7FFFFFFF) return fail("gather_rows_backward: T=%lld too large", (long long)T);
+  const dim3 g((unsigned)T), b((unsigned)std::min<int64_t>(256, (H / 8 + 63) / 64 * 64));
 #define MLORA_GRB(KT)                                                                                      \
   hipLaunchKernelGGL(gather_rows_backward_kernel<KT>, g, b, 0, as_stream(stream), (const u32x4*)dsel, H / 8, inv, T, \
                      k, offsets, E, (u32x4*)dh)
@@ -395,7 +428,8 @@ extern "C" int mlora_combine(const void* y, int64_t H, const void* w, int w_dtyp
   if (H % 8) return fail("combine: H=%lld must be a multiple of 8", (long long)H);
   if (k < 1 || E < 1) return fail("combine: k=%d, E=%d must be >= 1", k, E);
   if (T == 0) return 0;
-  const dim3 g(grid_for(T * (H / 8))), b(256);
+  if (T > 0x7FFFFFFF) return fail("combine: T=%lld too large", (long long)T);
+  const dim3 g((unsigned)T), b((unsigned)std::min<int64_t>(256, (H / 8 + 63) / 64 * 64));
   if (w_dtype != MLORA_DT_F32 && w_dtype != MLORA_DT_BF16) return fail("combine: weight dtype %d is not bf16/f32", w_dtype);
 #define MLORA_CMB(KT)                                                                                          \
   if (w_dtype == MLORA_DT_F32)                                                                                 \
