@@ -2,12 +2,15 @@
 //
 //   out[e, n, r] = bf16(scaling · sum over expert e's rows of g[row, n] · l[row, r])
 //
-// a product whose depth is the expert's row count.  One workgroup per (expert, 64 columns of g)
-// walks the expert's rows 64 at a time: a 64-row slice of g is transposed into LDS as [n][row]
-// (k = rows contiguous, the MFMA's layout) and the matching slice of l as [r][row]; each wave
-// accumulates a 16 x R block with v_mfma_f32_16x16x32_bf16 in fp32.  The next slice is loaded into
-// registers while the current one is multiplied.  Every output element has exactly one writer
-// and a fixed summation order: no atomics, the same bits every run.
+// a product whose depth is the expert's row count, bound by reading g once.  One workgroup per
+// (expert, 64 columns of g); each of its four waves walks its own 32-row chunks of the expert
+// (chunks wave, wave + 4, ...) on its own: the chunk's 32 x 64 slice of g and 32 x R slice of l are
+// loaded into registers two chunks ahead of use, transposed into the wave's own LDS area as [n][row]
+// and [r][row] (rows contiguous: the MFMA's k), and multiplied with v_mfma_f32_16x16x32_bf16 into
+// fp32.  Gathered row indices and row-scale indices are staged in LDS for 1024 rows at a time, so a
+// data load never waits behind an index load.  No barrier inside the chunk loop: a wave's LDS writes
+// and reads are ordered among themselves.  At the end the four waves' partial sums are added in a
+// fixed order (wave 0, 1, 2, 3): no atomics, the same bits every run.
 //
 // Rows of g may be gathered (row r read from g[gather[r] / gk]) and weighted by a per-row scale,
 // applied to the narrow operand: row r of l taken as bf16(row_scale[scale_index[r]] · l[r]).
@@ -17,15 +20,28 @@
 
 namespace mlora {
 
-constexpr int RB_N = 64;  // columns of g per workgroup
-constexpr int RPT = 2;                 // rows of g each thread loads per slice
-constexpr int RB_ROWS = 32 * RPT;      // rows per slice
-constexpr int RP_ = RB_ROWS + 8;
+constexpr int RB_N = 64;      // columns of g per workgroup
+constexpr int RB_CH = 32;     // rows per chunk, a wave's unit of work
+constexpr int RB_WAVES = 4;   // waves per workgroup
+constexpr int RB_IB = 1024;  // rows whose indices are staged in LDS at a time
+constexpr int RB_P = RB_CH + 8;  // LDS pitch of the transposed tiles in bf16 (80 bytes: the MFMA
+                                 // operand reads of 16 lanes cover the 64 banks once)
 
 __device__ __forceinline__ uint32_t lo2(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x05040100u); }
 __device__ __forceinline__ uint32_t hi2(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x07060302u); }
 
+// one chunk in registers: rows 4 (lane / 8) + q, columns 8 (lane % 8) .. +7 of g; NRB pieces of l
+// (piece lane + 64 q: row piece / (2 NRB), ranks 8 (piece % (2 NRB)) .. +7) with their row scales
 template <int NRB>
+struct RedChunk {
+  u32x4 g[4];
+  u32x4 l[NRB];
+  uint32_t ws[NRB];  // the dword holding each piece's row scale
+  uint32_t si[NRB];  // and that scale's index
+};
+// GATHER: rows of g read through gather; SCALED: l weighted by row_scale (compile-time, so that the
+// chunk loop has no branch: a load in a branch is copied at the join, and the copy waits for it)
+template <int NRB, bool GATHER, bool SCALED>
 __global__ __launch_bounds__(256) void grouped_reduce_kernel(const bf16* __restrict__ g, int64_t ldg,
                                                              const int64_t* __restrict__ gather, int gk,
                                                              const void* __restrict__ row_scale, int rs_dt,
@@ -35,110 +51,166 @@ __global__ __launch_bounds__(256) void grouped_reduce_kernel(const bf16* __restr
                                                              bf16* __restrict__ out, int64_t o_se, int64_t o_sn,
                                                              int64_t o_sr) {
   constexpr int R = NRB * 16;
-  __shared__ __attribute__((aligned(16))) bf16 Gs[RB_N * RP_];  // [n][row]
-  __shared__ __attribute__((aligned(16))) bf16 Ls[R * RP_];     // [r][row]
+  __shared__ __attribute__((aligned(16))) bf16 Gs[RB_WAVES][RB_N * RB_P];  // [n][row], one area per wave
+  __shared__ __attribute__((aligned(16))) bf16 Ls[RB_WAVES][R * RB_P];     // [r][row]
+  // a block of rows' indices, staged once for all waves: g's source rows and the row-scale indices
+  // (read from LDS, an index never shares the vector-memory counter with the data loads)
+  __shared__ uint32_t Is[GATHER ? RB_IB : 1];
+  __shared__ uint32_t Ss[SCALED ? RB_IB : 1];
+  static_assert(RB_WAVES * RB_N * RB_P * 2 >= RB_WAVES * RB_N * 16 * 4, "the partial sums fit in Gs");
   // gathered rows: consecutive workgroups take consecutive column blocks of one expert, so the rows
-  // they read at once are whole rows of the source (4 % faster at config 1); the expert's own rows:
-  // consecutive workgroups take consecutive experts (5 % faster)
-  const int e = gather != nullptr ? blockIdx.y : blockIdx.x;
-  const int n0 = (gather != nullptr ? blockIdx.x : blockIdx.y) * RB_N;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  // the expert's rows, clamped into [0, rows]
+  // they read at once are whole rows of the source; the expert's own rows: consecutive workgroups
+  // take consecutive experts
+  const int e = GATHER ? blockIdx.y : blockIdx.x;
+  const int n0 = (GATHER ? blockIdx.x : blockIdx.y) * RB_N;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: the chunk loop is a scalar loop
   const int64_t start = e == 0 ? 0 : min(max((int64_t)offsets[e - 1], (int64_t)0), rows);
   const int64_t end = min(max((int64_t)offsets[e], (int64_t)0), rows);
 
-  // this thread's RPT rows x 8 columns of g; the 4R threads that copy l (RPT rows x 8 ranks each)
-  // are spread over the waves where 256 divides evenly
-  constexpr int LSTRIDE = 256 % (4 * R) == 0 ? 256 / (4 * R) : 1;
-  const int gr = (tid >> 3) * RPT, gc = (tid & 7) * 8;
-  const int lo = tid / LSTRIDE;
-  const int lr = (lo / (R / 8)) * RPT, lc = (lo % (R / 8)) * 8;
-  const bool l_owner = tid % LSTRIDE == 0 && lo < 4 * R;
+  const int gq = (lane >> 3) * 4, gc = (lane & 7) * 8;
   const bool g_cols = n0 + gc < N;
+  const int gcc = g_cols ? n0 + gc : 0;  // a column that is always in g
+  int lr[NRB], lc[NRB];
+#pragma unroll
+  for (int q = 0; q < NRB; ++q) {
+    const int pc = lane + 64 * q;
+    lr[q] = pc / (2 * NRB);
+    lc[q] = (pc % (2 * NRB)) * 8;
+  }
 
-  u32x4 gv[RPT], lv[RPT];
-  float ws[RPT];
-  // the rows a slice reads, fetched one slice ahead so that no load waits on an index load: g's
-  // source row of each of this thread's RPT rows, and the row-scale index of each of its l rows
-  int64_t gsrc[RPT], sidx[RPT];
+  f32x4 acc[4][NRB];
 #pragma unroll
-  for (int q = 0; q < RPT; ++q) ws[q] = 1.f;
-  auto fetch_rows = [&](int64_t row0) {
+  for (int cb = 0; cb < 4; ++cb)
 #pragma unroll
-    for (int q = 0; q < RPT; ++q) {
-      const int64_t row = row0 + gr + q;
-      gsrc[q] = gather == nullptr || row >= end ? row : (int64_t)((uint32_t)gather[row] / (uint32_t)gk);
-      const int64_t lrow = row0 + lr + q;
-      sidx[q] = row_scale != nullptr && l_owner && lrow < end ? rs_idx[lrow] : 0;
-    }
-  };
-  auto load = [&](int64_t row0) {
-#pragma unroll
-    for (int q = 0; q < RPT; ++q) {
-      const int64_t row = row0 + gr + q;
-      gv[q] = (row < end && g_cols) ? *(const u32x4*)(g + gsrc[q] * ldg + n0 + gc) : u32x4{0u, 0u, 0u, 0u};
-      const int64_t lrow = row0 + lr + q;
-      if (l_owner) {
-        lv[q] = lrow < end ? *(const u32x4*)(l + lrow * ldl + lc) : u32x4{0u, 0u, 0u, 0u};
-        if (row_scale != nullptr && lrow < end)
-          ws[q] = rs_dt == MLORA_DT_F32 ? ((const float*)row_scale)[sidx[q]] : (float)((const bf16*)row_scale)[sidx[q]];
+    for (int j = 0; j < NRB; ++j) acc[cb][j] = f32x4{};
+  bf16* gs = Gs[wave];
+  bf16* ls = Ls[wave];
+
+  for (int64_t b0 = start; b0 < end; b0 += RB_IB) {
+    const int64_t b1 = min(end, b0 + (int64_t)RB_IB);
+    const int nb = (int)(b1 - b0);
+    if constexpr (GATHER || SCALED) {
+      __syncthreads();  // every wave is done with the previous block's indices
+      for (int i = tid; i < nb; i += 256) {
+        if constexpr (GATHER) Is[i] = (uint32_t)gather[b0 + i] / (uint32_t)gk;
+        if constexpr (SCALED) Ss[i] = (uint32_t)rs_idx[b0 + i];
       }
+      __syncthreads();
     }
-    fetch_rows(row0 + RB_ROWS);
-  };
-  auto store = [&]() {
-    if (row_scale != nullptr && l_owner) {  // l's rows weighted here, after the loads have had the MFMAs to land
+    const int chunks = (nb + RB_CH - 1) / RB_CH;
+    const int nc = chunks > wave ? (chunks - wave + RB_WAVES - 1) / RB_WAVES : 0;  // this wave's chunks
+    // Every load is unconditional: rows past the block's end read its last row (the values are dropped
+    // in consume), so no load sits in a branch, where the compiler would wait for it on the spot.
+    auto rel0 = [&](int c) { return (wave + RB_WAVES * c) * RB_CH; };  // the chunk's first row in the block
+    auto clamp = [&](int r) { return r < nb ? r : nb - 1; };
+    auto load = [&](RedChunk<NRB>& ch, int c) {
+      const int r0 = rel0(c);
 #pragma unroll
-      for (int q = 0; q < RPT; ++q)
+      for (int q = 0; q < 4; ++q) {
+        const int r = clamp(r0 + gq + q);
+        const int64_t src = GATHER ? (int64_t)Is[r] : b0 + r;
+        ch.g[q] = *(const u32x4*)(g + src * ldg + gcc);
+      }
 #pragma unroll
-        for (int m = 0; m < 4; ++m)
-          lv[q][m] = pack_bf16x2(bf16_bits_to_f32(lv[q][m] & 0xFFFFu) * ws[q], bf16_bits_to_f32(lv[q][m] >> 16) * ws[q]);
-    }
-    // transpose RPT rows x 8 columns into 8 columns x RPT rows, two rows per 32-bit store
-#pragma unroll
-    for (int pr = 0; pr < RPT; pr += 2)
-#pragma unroll
-      for (int m = 0; m < 4; ++m) {
-        *(uint32_t*)(Gs + (gc + 2 * m) * RP_ + gr + pr) = lo2(gv[pr][m], gv[pr + 1][m]);
-        *(uint32_t*)(Gs + (gc + 2 * m + 1) * RP_ + gr + pr) = hi2(gv[pr][m], gv[pr + 1][m]);
-        if (l_owner) {
-          *(uint32_t*)(Ls + (lc + 2 * m) * RP_ + lr + pr) = lo2(lv[pr][m], lv[pr + 1][m]);
-          *(uint32_t*)(Ls + (lc + 2 * m + 1) * RP_ + lr + pr) = hi2(lv[pr][m], lv[pr + 1][m]);
+      for (int q = 0; q < NRB; ++q) {
+        const int r = clamp(r0 + lr[q]);
+        ch.l[q] = *(const u32x4*)(l + (b0 + r) * ldl + lc[q]);
+        if constexpr (SCALED) {
+          // the dword holding the row's scale (a bf16 scale is one half of it, picked in consume): one
+          // load for either dtype
+          ch.si[q] = Ss[r];
+          ch.ws[q] = *(const uint32_t*)((const char*)row_scale +
+                                        (((uint64_t)ch.si[q] << (rs_dt == MLORA_DT_F32 ? 2 : 1)) & ~(uint64_t)3));
         }
       }
-  };
-
-  f32x4 acc[NRB];
+    };
+    auto consume = [&](RedChunk<NRB>& ch, int c) {
+      const int r0 = rel0(c);
 #pragma unroll
-  for (int j = 0; j < NRB; ++j) acc[j] = f32x4{};
-  if (start < end) {
-    fetch_rows(start);
-    load(start);
-  }
-  for (int64_t row0 = start; row0 < end; row0 += RB_ROWS) {
-    store();
-    __syncthreads();
-    if (row0 + RB_ROWS < end) load(row0 + RB_ROWS);
+      for (int q = 0; q < 4; ++q)
+        if (!(r0 + gq + q < nb && g_cols)) ch.g[q] = u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
-    for (int kk = 0; kk < RB_ROWS / 32; ++kk) {
-      const bf16x8 a = *(const bf16x8*)(Gs + (wave * 16 + (lane & 15)) * RP_ + kk * 32 + (lane >> 4) * 8);
+      for (int q = 0; q < NRB; ++q) {
+        if (!(r0 + lr[q] < nb)) ch.l[q] = u32x4{0u, 0u, 0u, 0u};
+        if constexpr (SCALED) {
+          const float w = rs_dt == MLORA_DT_F32 ? __uint_as_float(ch.ws[q])
+                                                : bf16_bits_to_f32((ch.si[q] & 1u) ? ch.ws[q] >> 16 : ch.ws[q] & 0xFFFFu);
 #pragma unroll
-      for (int j = 0; j < NRB; ++j) {
-        const bf16x8 b = *(const bf16x8*)(Ls + (j * 16 + (lane & 15)) * RP_ + kk * 32 + (lane >> 4) * 8);
-        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc[j], 0, 0, 0);
+          for (int m = 0; m < 4; ++m)
+            ch.l[q][m] = pack_bf16x2(bf16_bits_to_f32(ch.l[q][m] & 0xFFFFu) * w, bf16_bits_to_f32(ch.l[q][m] >> 16) * w);
+        }
       }
+      // 4 rows x 8 columns of g -> 8 columns x 4 rows (8 bytes per column)
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        *(u32x2*)(gs + (gc + 2 * m) * RB_P + gq) = u32x2{lo2(ch.g[0][m], ch.g[1][m]), lo2(ch.g[2][m], ch.g[3][m])};
+        *(u32x2*)(gs + (gc + 2 * m + 1) * RB_P + gq) = u32x2{hi2(ch.g[0][m], ch.g[1][m]), hi2(ch.g[2][m], ch.g[3][m])};
+      }
+#pragma unroll
+      for (int q = 0; q < NRB; ++q)
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          *(uint16_t*)(ls + (lc[q] + 2 * m) * RB_P + lr[q]) = (uint16_t)(ch.l[q][m] & 0xFFFFu);
+          *(uint16_t*)(ls + (lc[q] + 2 * m + 1) * RB_P + lr[q]) = (uint16_t)(ch.l[q][m] >> 16);
+        }
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's writes have landed
+      asm volatile("" ::: "memory");
+      bf16x8 b[NRB];
+#pragma unroll
+      for (int j = 0; j < NRB; ++j) b[j] = *(const bf16x8*)(ls + (j * 16 + (lane & 15)) * RB_P + (lane >> 4) * 8);
+#pragma unroll
+      for (int cb = 0; cb < 4; ++cb) {
+        const bf16x8 a = *(const bf16x8*)(gs + (cb * 16 + (lane & 15)) * RB_P + (lane >> 4) * 8);
+#pragma unroll
+        for (int j = 0; j < NRB; ++j) acc[cb][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[j], acc[cb][j], 0, 0, 0);
+      }
+      asm volatile("" ::: "memory");
+    };
+
+    // loads run two chunks ahead of use.  Both halves of the loop body run every iteration (a chunk
+    // past the wave's last holds only masked rows, which add zeros): a conditional half would make the
+    // compiler copy the loaded registers at the loop's back edge, and a copy waits for its load.
+    // sched_barrier keeps the phases in program order, so each wait leaves the later chunk in flight.
+    RedChunk<NRB> ca, cb_;
+    load(ca, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    load(cb_, 1);
+    __builtin_amdgcn_sched_barrier(0);
+    for (int c = 0; c < nc; c += 2) {
+      consume(ca, c);
+      __builtin_amdgcn_sched_barrier(0);
+      load(ca, c + 2);
+      __builtin_amdgcn_sched_barrier(0);
+      consume(cb_, c + 1);
+      __builtin_amdgcn_sched_barrier(0);
+      load(cb_, c + 3);
+      __builtin_amdgcn_sched_barrier(0);
     }
-    __syncthreads();
   }
-  // acc[j][v]: n = n0 + wave*16 + 4*(lane/16) + v, r = j*16 + lane%16
+
+  // the waves' partial sums, added in wave order; acc[cb][j][v] is column cb*16 + 4*(lane/16) + v,
+  // rank j*16 + lane%16
+  float* red = (float*)&Gs[0][0];
 #pragma unroll
-  for (int j = 0; j < NRB; ++j)
+  for (int j = 0; j < NRB; ++j) {
+    __syncthreads();
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int n = n0 + wave * 16 + 4 * (lane >> 4) + v;
-      const int r = j * 16 + (lane & 15);
-      if (n < N) out[(int64_t)e * o_se + (int64_t)n * o_sn + (int64_t)r * o_sr] = (bf16)(acc[j][v] * scaling);
+    for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) red[(wave * RB_N + cb * 16 + 4 * (lane >> 4) + v) * 16 + (lane & 15)] = acc[cb][j][v];
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < RB_N * 16 / 256; ++u) {
+      const int idx = tid + 256 * u, col = idx >> 4, r = idx & 15;
+      float s = red[idx];
+#pragma unroll
+      for (int w = 1; w < RB_WAVES; ++w) s += red[w * RB_N * 16 + idx];
+      const int n = n0 + col;
+      if (n < N) out[(int64_t)e * o_se + (int64_t)n * o_sn + (int64_t)(j * 16 + r) * o_sr] = (bf16)(s * scaling);
     }
+  }
 }
 
 }  // namespace mlora
@@ -154,6 +226,7 @@ static int grouped_reduce_impl(const void* g, int64_t ldg, const int64_t* gather
   if (row_scale != nullptr && (rs_idx == nullptr || (rs_dt != MLORA_DT_BF16 && rs_dt != MLORA_DT_F32)))
     return fail("grouped_reduce_gather: a row scale needs its index and a bf16/f32 dtype (got %d)", rs_dt);
   if (E < 1 || E > 65535) return fail("grouped_reduce: E=%d outside [1, 65535]", E);
+  if (rows < 0 || rows > (int64_t)0xFFFFFFFFu) return fail("grouped_reduce: rows=%lld outside [0, 2^32)", (long long)rows);
   if (N < 8 || N % 8 || ldg < N || ldg % 8 || ((uintptr_t)g & 15u))
     return fail("grouped_reduce: g needs N (%d) and its row stride (%lld) multiples of 8, 16-byte aligned", N, (long long)ldg);
   if (R < 16 || R > 64 || R % 16) return fail("grouped_reduce: R=%d must be 16, 32, 48 or 64", R);
@@ -161,15 +234,21 @@ static int grouped_reduce_impl(const void* g, int64_t ldg, const int64_t* gather
   const unsigned nblk = (unsigned)((N + RB_N - 1) / RB_N);
   const dim3 grid(gather != nullptr ? nblk : (unsigned)E, gather != nullptr ? (unsigned)E : nblk), block(256);
   hipStream_t s = as_stream(stream);
-#define MLORA_RED(NRB)                                                                                               \
-  hipLaunchKernelGGL(grouped_reduce_kernel<NRB>, grid, block, 0, s, (const bf16*)g, ldg, gather, gk, row_scale, rs_dt,   \
-                     rs_idx, (const bf16*)l, ldl, rows, N, scaling, offsets, (bf16*)out, o_se, o_sn, o_sr)
-  switch (R / 16) {
-    case 1: MLORA_RED(1); break;
-    case 2: MLORA_RED(2); break;
-    case 3: MLORA_RED(3); break;
-    default: MLORA_RED(4); break;
+#define MLORA_RED(NRB, GA, SC)                                                                                       \
+  hipLaunchKernelGGL((grouped_reduce_kernel<NRB, GA, SC>), grid, block, 0, s, (const bf16*)g, ldg, gather, gk, row_scale, \
+                     rs_dt, rs_idx, (const bf16*)l, ldl, rows, N, scaling, offsets, (bf16*)out, o_se, o_sn, o_sr)
+#define MLORA_RED_R(GA, SC)            \
+  switch (R / 16) {                    \
+    case 1: MLORA_RED(1, GA, SC); break; \
+    case 2: MLORA_RED(2, GA, SC); break; \
+    case 3: MLORA_RED(3, GA, SC); break; \
+    default: MLORA_RED(4, GA, SC); break; \
   }
+  if (gather != nullptr && row_scale != nullptr) MLORA_RED_R(true, true)
+  else if (gather != nullptr) MLORA_RED_R(true, false)
+  else if (row_scale != nullptr) MLORA_RED_R(false, true)
+  else MLORA_RED_R(false, false)
+#undef MLORA_RED_R
 #undef MLORA_RED
   return launch_status("grouped_reduce");
 }
