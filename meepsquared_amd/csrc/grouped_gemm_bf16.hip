@@ -65,6 +65,12 @@ static_assert(FM >= 1 && FN >= 1 && (2 * FM) % WAVES_N == 0, "tile shape");
 typedef __attribute__((address_space(3))) void lds_void;
 
 constexpr int kSmallLastE = 1024;  // experts up to which the small last tiles are scheduled last
+// Tall items: an expert whose rows leave a last tile of at most XR rows after its full tiles has that
+// remainder merged into its last full tile, which then holds BM + XR rows at most; each wave takes one
+// more 32 x 32 block (the extra rows x its column block wm * WAVES_N + wn), +12.5 % MFMA work on that
+// item instead of a near-empty item of its own (which costs most of a full one: its stages are bound
+// by the copy latency).  The extra rows' x tile sits at the end of each ring slot.
+constexpr int XR = 32;
 
 // [row][k] tiles (rows of BK bf16, CPR chunks of 16 bytes): chunk c of row r in slot c ^ f(r), with f
 // spreading the 16 rows one MFMA operand read touches over 16 distinct 16-byte bank groups
@@ -122,11 +128,13 @@ __device__ __forceinline__ void scan_wave(int* v, int E, int lane) {  // inclusi
   }
 }
 
-__device__ __forceinline__ void build_tile_ends(const GemmArgs& p, int* tend, int* sfx, bool small_last, int tid) {
+__device__ __forceinline__ void build_tile_ends(const GemmArgs& p, int* tend, int* sfx, bool small_last, bool tall,
+                                                int tid) {
   const int E = p.E;
   for (int e = tid; e < E; e += kThreads) {
     const int64_t c = row_start(p, e + 1) - row_start(p, e);
-    const int nt = c > 0 ? (int)((c + BM - 1) / BM) : 0;
+    int nt = c > 0 ? (int)((c + BM - 1) / BM) : 0;
+    if (tall && nt >= 2 && c - (int64_t)(nt - 1) * BM <= XR) --nt;  // the remainder joins the last full tile
     const int small = small_last && nt > 0 && c - (int64_t)(nt - 1) * BM <= BM / 2;
     tend[e] = nt - small;
     if (small_last) sfx[e] = small;
@@ -149,7 +157,7 @@ __device__ __forceinline__ int first_above(const int* v, int E, int t) {  // the
 // work item (tile t, column block) -> wave-uniform expert, rows and columns; small: t counts the
 // small last tiles
 __device__ __forceinline__ Item decode(const GemmArgs& p, int64_t item, int nb, const int* tend, const int* sfx,
-                                       bool small) {
+                                       bool small, bool tall) {
   const int t = (int)(item / nb);
   Item it;
   it.nblk = (int)(item - (int64_t)t * nb);
@@ -163,7 +171,9 @@ __device__ __forceinline__ Item decode(const GemmArgs& p, int64_t item, int nb, 
                     (it.e == 0 ? 0 : __builtin_amdgcn_readfirstlane(tend[it.e - 1]));
     it.row0 = row_start(p, it.e) + (int64_t)big * BM;
   }
-  it.mrows = (int)min((int64_t)BM, row_start(p, it.e + 1) - it.row0);
+  // an item left with at most BM + XR rows is the expert's last (a tall one when it has more than BM)
+  const int64_t left = row_start(p, it.e + 1) - it.row0;
+  it.mrows = (int)(left <= BM + (tall ? XR : 0) ? left : (int64_t)BM);
   it.n0 = it.nblk * BN;
   return it;
 }
@@ -198,15 +208,16 @@ struct WTile {
 template <int WT>
 __device__ __forceinline__ int swz_q(int n) { return WTile<WT>::kFp8 ? (n >> 2) & 3 : (n >> 3) & 1; }
 
-template <int NRB, int WT = kWBf16>
+template <int NRB, int WT = kWBf16, bool TALL = false>
 struct SlotSize {
   static constexpr int RD = (NRB == 3 ? 4 : NRB) * 16;
-  static constexpr int kElems = BM * BK + WTile<WT>::Elems + RD * BK;
+  static constexpr int kXOff = BM * BK + WTile<WT>::Elems + RD * BK;  // the tall rows' x tile [XR][BK]
+  static constexpr int kElems = kXOff + (TALL ? XR * BK : 0);
 };
 
 // Per-lane DMA addressing of one item, fixed for its whole K loop: byte offsets at k = 0 and the
 // k of each lane's chunk (a huge k marks a column past N: never in range).
-template <bool BKC, int NRB, int WT>
+template <bool BKC, int NRB, int WT, bool TALL = false>
 struct Feed {
   static_assert(WT == kWBf16 || BKC, "fp8 and NF4 stacks are read with k contiguous");
   static constexpr int RP = NRB * 16;
@@ -216,6 +227,14 @@ struct Feed {
   // this wave's copies per stage: XI of x, WI of the stack, one (lane-masked) of A^T
   static constexpr int PS = XI + WI + (NRB > 0 ? 1 : 0);
   rsrc_t rx, rw, ra, rs;  // rs: the expert's scales along k (kWFp8K)
+  // TALL: the extra rows' x tile, copied by waves 0 .. XR * CPR / 64 - 1 (one instruction each) when the
+  // item holds more than BM rows.  Waves issue different counts then: the ring waits for every copy
+  // of a wave (vmcnt 0) with two slots, so the counts need not match.
+  static constexpr int kTallWaves = XR * CPR / 64;
+  static_assert(!TALL || (STAGES == 2 && (XR * CPR) % 64 == 0 && kTallWaves <= NW), "tall rows' copies");
+  uint32_t to;
+  int tk, td;
+  bool t_on;
   uint32_t xo[XI], wo[WI], ao;
   int xk[XI], wk[WI], ak;
   int xd[XI], wd[WI], ad;  // LDS element offset of each instruction's 64 lanes within the slot
@@ -264,6 +283,18 @@ struct Feed {
       wd[q] = BM * BK + instr * 512;
     }
     wstep = WTile<WT>::kFp8 ? 1 : BKC ? 2 : 2 * p.w_sk;
+    if constexpr (TALL) {
+      t_on = mrows > BM && wave < kTallWaves;
+      const int ci = wave * 64 + lane, row = ci / CPR, c = (ci % CPR) ^ swz_f(row);
+      if (p.gather == nullptr) {
+        to = (uint32_t)(((BM + row) * p.ldx + c * 8) * 2);  // rows past the item: past its resource, zeros
+      } else {
+        const int64_t src = BM + row < mrows ? p.gather[row0 + BM + row] / p.gk : -1;
+        to = src >= 0 ? (uint32_t)((src * p.ldx + c * 8) * 2) : kOob;
+      }
+      tk = c * 8;
+      td = SlotSize<NRB, WT, true>::kXOff + wave * 512;
+    }
     if constexpr (NRB > 0) {
       // wave w copies chunks [w * CPW, (w + 1) * CPW) of the A^T tile: lanes of one 64-chunk
       // instruction block, the others masked off (their LDS bytes belong to other waves)
@@ -292,6 +323,9 @@ struct Feed {
 #pragma unroll
       for (int q = 0; q < XI; ++q)
         dma16(rx, slot + xd[q], xk[q] + k0 < p.K ? xo[q] + (uint32_t)(k0 * 2) : kOob);
+      if constexpr (TALL) {
+        if (t_on) dma16(rx, slot + td, tk + k0 < p.K ? to + (uint32_t)(k0 * 2) : kOob);
+      }
     }
     if constexpr (PART == 1) {
 #pragma unroll
@@ -483,11 +517,16 @@ __device__ __forceinline__ bf16x8 nf4_decode(uint32_t x, const uint32_t (&lo)[4]
 // The MFMAs of one stage held in `slot` for a wave with AM live row blocks.
 // The copies of the next stage (into nslot) are issued in three parts after the first MFMA steps:
 // issued back to back they fill the texture unit's queues and hold the wave in front of its MFMAs.
-template <int AM, bool BKC, int NRB, int WT>
+// TL: a tall item (BM + up to XR rows): one more MFMA per step into tacc, the extra rows x this wave's
+// column block wm (and their x A_e in tlacc, by waves (0, 0) and (0, 1), one 16-row half each)
+template <int AM, bool BKC, int NRB, int WT, bool TL, class F>
 __device__ __forceinline__ void compute(const GemmArgs& p, const bf16* slot, int lane, int wm, int wn,
                                         f32x16 (&acc)[FM][FN], f32x4 (&lacc)[kLS][NRB > 0 ? NRB : 1],
+                                        f32x16& tacc, f32x4 (&tlacc)[NRB > 0 ? NRB : 1],
                                         Nf4Pipe& nf, const float* code, float off, int kt,
-                                        const Feed<BKC, NRB, WT>& f, bf16* nslot, int nkt) {
+                                        const F& f, bf16* nslot, int nkt) {
+  static_assert(!TL || (AM == FM && FN == 2 && WAVES_M == 2 && WAVES_N >= 2), "tall items: 2 x 4 waves, full row blocks");
+  constexpr int kXOff = SlotSize<NRB, WT, true>::kXOff;
   const bf16* as = slot;
   const bf16* bs = slot + BM * BK;
   uint32_t tlo[WT == kWNf4 ? FN : 1][4], thi[WT == kWNf4 ? FN : 1][4];
@@ -527,6 +566,10 @@ __device__ __forceinline__ void compute(const GemmArgs& p, const bf16* slot, int
 #pragma unroll
         for (int j = 0; j < FN; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[j], af[i], acc[i][j], 0, 0, 0);
+      if constexpr (TL) {
+        const bf16x8 at = *(const bf16x8*)(slot + kXOff + swz_rk(lane & 31, kk * 2 + (lane >> 5)));
+        tacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wm == 0 ? bfr[0] : bfr[1], at, tacc, 0, 0, 0);
+      }
       constexpr int last = BK / 16 - 1;
       if (kk <= 2 || kk == last) __builtin_amdgcn_sched_barrier(0);
       if (kk == 0) f.template issue_part<0>(p, nslot, nkt);
@@ -552,6 +595,14 @@ __device__ __forceinline__ void compute(const GemmArgs& p, const bf16* slot, int
               lacc[q][rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf, ar[rb], lacc[q][rb], 0, 0, 0);
           }
         }
+        if constexpr (TL) {
+          if (wm == 0 && wn < 2) {
+            const bf16x8 xf = *(const bf16x8*)(slot + kXOff + swz_rk(wn * 16 + (lane & 15), ls * 4 + (lane >> 4)));
+#pragma unroll
+            for (int rb = 0; rb < NRB; ++rb)
+              tlacc[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf, ar[rb], tlacc[rb], 0, 0, 0);
+          }
+        }
       }
     }
   }
@@ -559,50 +610,51 @@ __device__ __forceinline__ void compute(const GemmArgs& p, const bf16* slot, int
 
 // One iteration of the K loop: wait for this wave's copies of stage kt (slot S), publish every
 // wave's with a barrier, queue stage kt + STAGES - 1 into the slot read one iteration ago, multiply.
-template <int S, int AM, bool BKC, int NRB, int WT>
-__device__ __forceinline__ void stage(const GemmArgs& p, const Feed<BKC, NRB, WT>& f, bf16* const (&slots)[STAGES], int kt,
+template <int S, int AM, bool BKC, int NRB, int WT, bool TL, class F>
+__device__ __forceinline__ void stage(const GemmArgs& p, const F& f, bf16* const (&slots)[STAGES], int kt,
                                       int lane, int wm, int wn, f32x16 (&acc)[FM][FN],
-                                      f32x4 (&lacc)[kLS][NRB > 0 ? NRB : 1], Nf4Pipe& nf, const float* code,
-                                      float off) {
-  wait_vm<Feed<BKC, NRB, WT>::PS * (STAGES - 2)>();  // stages kt+1, kt+2 may stay in flight
+                                      f32x4 (&lacc)[kLS][NRB > 0 ? NRB : 1], f32x16& tacc,
+                                      f32x4 (&tlacc)[NRB > 0 ? NRB : 1], Nf4Pipe& nf, const float* code, float off) {
+  wait_vm<F::PS * (STAGES - 2)>();  // stages kt+1, kt+2 may stay in flight
   stage_barrier();
-  compute<AM, BKC, NRB, WT>(p, slots[S], lane, wm, wn, acc, lacc, nf, code, off, kt, f,
-                            slots[(S + STAGES - 1) % STAGES], kt + STAGES - 1);
+  compute<AM, BKC, NRB, WT, TL>(p, slots[S], lane, wm, wn, acc, lacc, tacc, tlacc, nf, code, off, kt, f,
+                                slots[(S + STAGES - 1) % STAGES], kt + STAGES - 1);
 }
 
 // The K loop of one item, unrolled by the ring depth so every slot index is a constant.
-template <int AM, bool BKC, int NRB, int WT>
-__device__ __forceinline__ void kloop(const GemmArgs& p, const Feed<BKC, NRB, WT>& f, bf16* const (&slots)[STAGES], int nk,
+template <int AM, bool BKC, int NRB, int WT, bool TL = false, class F>
+__device__ __forceinline__ void kloop(const GemmArgs& p, const F& f, bf16* const (&slots)[STAGES], int nk,
                                       int lane, int wm, int wn, f32x16 (&acc)[FM][FN],
-                                      f32x4 (&lacc)[kLS][NRB > 0 ? NRB : 1], Nf4Pipe& nf, const float* code,
-                                      float off) {
+                                      f32x4 (&lacc)[kLS][NRB > 0 ? NRB : 1], f32x16& tacc,
+                                      f32x4 (&tlacc)[NRB > 0 ? NRB : 1], Nf4Pipe& nf, const float* code, float off) {
   int kt = 0;
   if constexpr (STAGES == 4) {
     for (; kt + STAGES <= nk; kt += STAGES) {
-      stage<0, AM, BKC, NRB, WT>(p, f, slots, kt, lane, wm, wn, acc, lacc, nf, code, off);
-      stage<1, AM, BKC, NRB, WT>(p, f, slots, kt + 1, lane, wm, wn, acc, lacc, nf, code, off);
-      stage<2, AM, BKC, NRB, WT>(p, f, slots, kt + 2, lane, wm, wn, acc, lacc, nf, code, off);
-      stage<3, AM, BKC, NRB, WT>(p, f, slots, kt + 3, lane, wm, wn, acc, lacc, nf, code, off);
+      stage<0, AM, BKC, NRB, WT, TL>(p, f, slots, kt, lane, wm, wn, acc, lacc, tacc, tlacc, nf, code, off);
+      stage<1, AM, BKC, NRB, WT, TL>(p, f, slots, kt + 1, lane, wm, wn, acc, lacc, tacc, tlacc, nf, code, off);
+      stage<2, AM, BKC, NRB, WT, TL>(p, f, slots, kt + 2, lane, wm, wn, acc, lacc, tacc, tlacc, nf, code, off);
+      stage<3, AM, BKC, NRB, WT, TL>(p, f, slots, kt + 3, lane, wm, wn, acc, lacc, tacc, tlacc, nf, code, off);
     }
     const int rem = nk - kt;  // 0 .. 3 stages left
-    if (rem > 0) stage<0, AM, BKC, NRB, WT>(p, f, slots, kt, lane, wm, wn, acc, lacc, nf, code, off);
-    if (rem > 1) stage<1, AM, BKC, NRB, WT>(p, f, slots, kt + 1, lane, wm, wn, acc, lacc, nf, code, off);
-    if (rem > 2) stage<2, AM, BKC, NRB, WT>(p, f, slots, kt + 2, lane, wm, wn, acc, lacc, nf, code, off);
+    if (rem > 0) stage<0, AM, BKC, NRB, WT, TL>(p, f, slots, kt, lane, wm, wn, acc, lacc, tacc, tlacc, nf, code, off);
+    if (rem > 1) stage<1, AM, BKC, NRB, WT, TL>(p, f, slots, kt + 1, lane, wm, wn, acc, lacc, tacc, tlacc, nf, code, off);
+    if (rem > 2) stage<2, AM, BKC, NRB, WT, TL>(p, f, slots, kt + 2, lane, wm, wn, acc, lacc, tacc, tlacc, nf, code, off);
   } else {
     for (; kt + 2 <= nk; kt += 2) {
-      stage<0, AM, BKC, NRB, WT>(p, f, slots, kt, lane, wm, wn, acc, lacc, nf, code, off);
-      stage<1, AM, BKC, NRB, WT>(p, f, slots, kt + 1, lane, wm, wn, acc, lacc, nf, code, off);
+      stage<0, AM, BKC, NRB, WT, TL>(p, f, slots, kt, lane, wm, wn, acc, lacc, tacc, tlacc, nf, code, off);
+      stage<1, AM, BKC, NRB, WT, TL>(p, f, slots, kt + 1, lane, wm, wn, acc, lacc, tacc, tlacc, nf, code, off);
     }
-    if (kt < nk) stage<0, AM, BKC, NRB, WT>(p, f, slots, kt, lane, wm, wn, acc, lacc, nf, code, off);
+    if (kt < nk) stage<0, AM, BKC, NRB, WT, TL>(p, f, slots, kt, lane, wm, wn, acc, lacc, tacc, tlacc, nf, code, off);
   }
 }
 
-template <bool BKC, int NRB, int WT>
+template <bool BKC, int NRB, int WT, bool TALL = false>
 __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_kernel(GemmArgs p) {
   constexpr int RP = NRB * 16;
   constexpr int LP = RP + 8;
-  constexpr int SE = SlotSize<NRB, WT>::kElems;
-  static_assert(BM * LP <= SE && BN * LP + (STAGES == 4 ? 0 : BN * 3) <= SE,
+  constexpr int SE = SlotSize<NRB, WT, TALL>::kElems;
+  constexpr int BMT = BM + (TALL ? XR : 0);  // the most rows an item holds
+  static_assert(BMT * LP <= SE && BN * LP + (STAGES == 4 ? 0 : BN * 3) <= SE,
                 "the epilogue's low, B^T, column-scale and bias tiles fit in the slots they reuse");
   __shared__ __attribute__((aligned(16))) bf16 slot0[SE];
   __shared__ __attribute__((aligned(16))) bf16 slot1[SE];
@@ -641,7 +693,7 @@ __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_ker
   if constexpr (WT == kWNf4T) {
     for (int c = tid0; c < 16; c += kThreads) code[c] = p.nf4_code[c];
   }
-  build_tile_ends(p, tile_map, sfx, small_last, tid0);
+  build_tile_ends(p, tile_map, sfx, small_last, TALL, tid0);
   const int nb = (p.N + BN - 1) / BN;
   // each XCD takes one contiguous eighth of the full tiles' items, then one eighth of the small tiles'
   const int64_t nbig = (int64_t)__builtin_amdgcn_readfirstlane(tile_map[E - 1]) * nb;
@@ -660,7 +712,7 @@ __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_ker
     int tid = tid0;
     asm volatile("" : "+v"(tid));
     const int lane = tid & 63;
-    const Item it = decode(p, item, nb, tile_map, sfx, small);
+    const Item it = decode(p, item, nb, tile_map, sfx, small, TALL);
     const int e = it.e, n0 = it.n0, mrows = it.mrows;
     const int64_t row0 = it.row0;
     const int ncols = min(BN, p.N - n0);
@@ -668,7 +720,7 @@ __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_ker
     const int am = min(FM, max(0, (mb - wm + WAVES_M - 1) / WAVES_M));
     const int an = min(FN, max(0, (nbk - wn + WAVES_N - 1) / WAVES_N));
 
-    Feed<BKC, NRB, WT> f;
+    Feed<BKC, NRB, WT, TALL> f;
     f.rx = p.gather == nullptr ? make_rsrc(p.x + row0 * p.ldx, (int64_t)mrows * p.ldx * 2)
                                : make_rsrc(p.x, p.xrows * p.ldx * 2);
     {
@@ -692,6 +744,11 @@ __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_ker
     for (int q = 0; q < kLS; ++q)
 #pragma unroll
       for (int j = 0; j < (NRB > 0 ? NRB : 1); ++j) lacc[q][j] = f32x4{};
+    f32x16 tacc = f32x16{};  // a tall item's extra rows x column block wm * WAVES_N + wn
+    f32x4 tlacc[NRB > 0 ? NRB : 1];
+#pragma unroll
+    for (int j = 0; j < (NRB > 0 ? NRB : 1); ++j) tlacc[j] = f32x4{};
+    const bool tall = TALL && mrows > BM;
 
     Nf4Pipe nf;
     if constexpr (WT == kWNf4T) nf.planes(code);  // (the tile map's barrier published the code book)
@@ -712,17 +769,25 @@ __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_ker
     for (int s = 0; s < STAGES - 1; ++s) f.issue(p, slots[s], s);
 
     switch (am) {
-      case FM: kloop<FM, BKC, NRB, WT>(p, f, slots, nk, lane, wm, wn, acc, lacc, nf, code, off); break;
+      case FM:
+        if constexpr (TALL) {
+          if (tall) {
+            kloop<FM, BKC, NRB, WT, true>(p, f, slots, nk, lane, wm, wn, acc, lacc, tacc, tlacc, nf, code, off);
+            break;
+          }
+        }
+        kloop<FM, BKC, NRB, WT>(p, f, slots, nk, lane, wm, wn, acc, lacc, tacc, tlacc, nf, code, off);
+        break;
 #if (256 / MLORA_DMA_WM / 32) >= 4
-      case 3: kloop<3, BKC, NRB, WT>(p, f, slots, nk, lane, wm, wn, acc, lacc, nf, code, off); break;
+      case 3: kloop<3, BKC, NRB, WT>(p, f, slots, nk, lane, wm, wn, acc, lacc, tacc, tlacc, nf, code, off); break;
 #endif
 #if (256 / MLORA_DMA_WM / 32) >= 3
-      case 2: kloop<2, BKC, NRB, WT>(p, f, slots, nk, lane, wm, wn, acc, lacc, nf, code, off); break;
+      case 2: kloop<2, BKC, NRB, WT>(p, f, slots, nk, lane, wm, wn, acc, lacc, tacc, tlacc, nf, code, off); break;
 #endif
 #if (256 / MLORA_DMA_WM / 32) >= 2
-      case 1: kloop<1, BKC, NRB, WT>(p, f, slots, nk, lane, wm, wn, acc, lacc, nf, code, off); break;
+      case 1: kloop<1, BKC, NRB, WT>(p, f, slots, nk, lane, wm, wn, acc, lacc, tacc, tlacc, nf, code, off); break;
 #endif
-      default: kloop<0, BKC, NRB, WT>(p, f, slots, nk, lane, wm, wn, acc, lacc, nf, code, off); break;
+      default: kloop<0, BKC, NRB, WT>(p, f, slots, nk, lane, wm, wn, acc, lacc, tacc, tlacc, nf, code, off); break;
     }
     wait_vm<0>();     // the zero-filled copies queued past the end of K
     __syncthreads();  // every wave is done with the ring (all copies waited for in the loop)
@@ -753,6 +818,13 @@ __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_ker
         rs[i] = p.row_scale_dt == MLORA_DT_F32 ? ((const float*)p.row_scale)[si] : (float)((const bf16*)p.row_scale)[si];
       }
     }
+    float rs_t = 1.f;  // the tall rows' output scale
+    if constexpr (TALL) {
+      if (tall && p.row_scale != nullptr && BM + (lane & 31) < mrows) {
+        const int64_t si = p.gather[row0 + BM + (lane & 31)];
+        rs_t = p.row_scale_dt == MLORA_DT_F32 ? ((const float*)p.row_scale)[si] : (float)((const bf16*)p.row_scale)[si];
+      }
+    }
     if constexpr (NRB > 0) {
 #pragma unroll
       for (int q = 0; q < kLS; ++q) {
@@ -763,6 +835,15 @@ __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_ker
 #pragma unroll
           for (int v = 0; v < 4; ++v)
             Ls[(rbase + 4 * (lane >> 4) + v) * LP + rb * 16 + (lane & 15)] = (bf16)lacc[q][rb][v];
+      }
+      if constexpr (TALL) {
+        if (tall && wm == 0 && wn < 2) {
+#pragma unroll
+          for (int rb = 0; rb < NRB; ++rb)
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+              Ls[(BM + wn * 16 + 4 * (lane >> 4) + v) * LP + rb * 16 + (lane & 15)] = (bf16)tlacc[rb][v];
+        }
       }
       if constexpr (!kPreB) {
         const rsrc_t rbt = make_rsrc(p.bt + (int64_t)e * p.bt_se, (int64_t)p.N * p.bt_sn * 2);
@@ -777,7 +858,7 @@ __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_ker
     wait_vm<0>();  // the row scales (and every other load) are in before the first store
     if constexpr (NRB > 0) {
       if (p.low != nullptr && it.nblk == 0) {
-        for (int c = tid; c < BM * RP / 8; c += kThreads) {
+        for (int c = tid; c < BMT * RP / 8; c += kThreads) {
           const int m = c / (RP / 8), rc = (c - m * (RP / 8)) * 8;
           if (m < mrows) *(u32x4*)(p.low + (row0 + m) * p.ldl + rc) = *(const u32x4*)(Ls + m * LP + rc);
         }
@@ -787,20 +868,26 @@ __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_ker
     const bool plain = !col_scale && cexp == 1.f && p.row_scale == nullptr && !has_bias;
     // the item's rows of out through a buffer resource: 32-bit offsets, stores past its rows dropped
     const rsrc_t ro = make_rsrc(p.out + row0 * p.ldo, (int64_t)mrows * p.ldo * 2);
+    // the output blocks: row block i (rows (i * WAVES_M + wm) * 32 ..) x column block j * WAVES_N + wn,
+    // and for a tall item one more, i = FM: its extra rows x column block wm * WAVES_N + wn
 #pragma unroll
-    for (int i = 0; i < FM; ++i) {
-      const int row = (i * WAVES_M + wm) * 32 + (lane & 31);
-      if (i >= am) continue;
+    for (int i = 0; i < FM + (TALL ? 1 : 0); ++i) {
+      const bool tb = TALL && i == FM;
+      if (tb ? !tall : i >= am) continue;
+      const int rbase = tb ? BM : (i * WAVES_M + wm) * 32;
+      const int row = rbase + (lane & 31);
       const uint32_t orow = (uint32_t)(row * p.ldo * 2);
 #pragma unroll
       for (int j = 0; j < FN; ++j) {
-        if (j >= an) continue;
+        if (j >= an || (tb && j != wm)) continue;
+        const f32x16& av = tb ? tacc : acc[i < FM ? i : 0][j];
+        const float rsv = tb ? rs_t : rs[i < FM ? i : 0];
         f32x16 t = f32x16{};
         if constexpr (NRB > 0) {
           if (lora_on) {
 #pragma unroll
             for (int rk = 0; rk < NRB; ++rk) {
-              const bf16x8 lf = *(const bf16x8*)(Ls + ((i * WAVES_M + wm) * 32 + (lane & 31)) * LP + rk * 16 + (lane >> 5) * 8);
+              const bf16x8 lf = *(const bf16x8*)(Ls + (rbase + (lane & 31)) * LP + rk * 16 + (lane >> 5) * 8);
               const int nr = (j * WAVES_N + wn) * 32 + (lane & 31);
               const bf16x8 bfr = kPreB ? *(const bf16x8*)(lbt + nr * 16 + (((lane >> 5) ^ ((nr >> 2) & 1)) << 3))
                                        : *(const bf16x8*)(Lb + nr * LP + rk * 16 + (lane >> 5) * 8);
@@ -817,7 +904,7 @@ __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_ker
           for (int g = 0; g < 4; ++g) {
             float o[4];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) o[q] = __builtin_fmaf(p.scaling, t[4 * g + q], acc[i][j][4 * g + q]);
+            for (int q = 0; q < 4; ++q) o[q] = __builtin_fmaf(p.scaling, t[4 * g + q], av[4 * g + q]);
             pk[g] = u32x2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
           }
         } else {
@@ -834,7 +921,7 @@ __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_ker
             float o[4];
 #pragma unroll
             for (int q = 0; q < 4; ++q)
-              o[q] = (acc[i][j][4 * g + q] * c[q] + p.scaling * t[4 * g + q]) * rs[i] + bias[q];
+              o[q] = (av[4 * g + q] * c[q] + p.scaling * t[4 * g + q]) * rsv + bias[q];
             pk[g] = u32x2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
           }
         }
@@ -874,9 +961,21 @@ static_assert(STAGES * SlotSize<1>::kElems * 2 + BN * 16 * 2 + 4096 * 4 <= 16384
               "with one rank block: the slots, the B^T tile and the largest tile map fit in LDS");
 static_assert(WTile<kWNf4>::RowBytes * 2 == 64, "an NF4 stage is one block of 64 codes per row");
 
+// tall items: bf16 stacks, rank 16 or none, two-slot ring, and a tile map small enough to sit beside the
+// larger slots (the small-tile counts included)
+static_assert(STAGES * SlotSize<1, kWBf16, true>::kElems * 2 + BN * 16 * 2 + kSmallLastE * 8 <= 163840,
+              "tall items: the slots, the B^T tile and the tile map fit in LDS");
+// (k-contiguous stacks only: the transposing reads of the other orientation need more registers,
+// and its K loop then spills, 22-25 % slower than without tall items)
 template <bool BKC, int NRB, int WT>
+constexpr bool kTallOn = BKC && STAGES == 2 && WT == kWBf16 && NRB <= 1 && WAVES_M == 2 && WAVES_N >= 2 && FN == 2;
+
+template <bool BKC, int NRB, int WT, bool TALL = false>
 static int launch_t(const GemmArgs& a, hipStream_t s) {
-  auto kern = grouped_gemm_bf16_kernel<BKC, NRB, WT>;
+  if constexpr (kTallOn<BKC, NRB, WT> && !TALL) {
+    if (a.E <= kSmallLastE) return launch_t<BKC, NRB, WT, true>(a, s);
+  }
+  auto kern = grouped_gemm_bf16_kernel<BKC, NRB, WT, TALL>;
   const size_t lds = lds_bytes(a.E, WT);
   static std::mutex mu;
   static std::unordered_map<int64_t, int> grid_cache;

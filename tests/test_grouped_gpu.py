@@ -125,6 +125,32 @@ def test_the_product_with_adapters_and_its_gradients_match_pytorch(is_transposed
         torch.testing.assert_close(a.float(), b.float(), atol=1e-2 * b.float().abs().max().item(), rtol=0, msg=name)
 
 
+@pytest.mark.parametrize("is_transposed", [False, True])
+def test_tall_items_match_one_product_per_expert(is_transposed):
+    """Groups whose last tile holds at most 32 rows past a full one (257, 288, 513, 544 rows) are run
+    as one item of up to 288 rows; 289 and 545 rows keep a tile of their own.  Output, input gradient
+    and both adapter gradients against the oracle, with a bias and a column block cut short (N = 320)."""
+    torch.manual_seed(0)
+    rows_per_expert = [257, 288, 289, 0, 545, 544, 513, 256, 1, 800, 33, 290]
+    K, N, rank = 160, 320, 16
+    experts = len(rows_per_expert)
+    offsets = offsets_of(rows_per_expert)
+    x = torch.randn(sum(rows_per_expert), K, device="cuda", dtype=torch.bfloat16).requires_grad_()
+    shape = (experts, K, N) if is_transposed else (experts, N, K)
+    weight = torch.randn(shape, device="cuda", dtype=torch.bfloat16) * 0.05
+    lhs, rhs = adapters(experts, K, N, rank, is_transposed)
+    bias = torch.randn(experts, N, device="cuda", dtype=torch.bfloat16)
+    got, expected = run_both(x, weight, None, offsets, is_transposed, lhs, rhs, 2.0, bias)
+    for name, a, b in zip(("out", "grad_x", "grad_lhs", "grad_rhs"), got, expected):
+        assert rel(a, b) < BF16_TOL, (name, rel(a, b))
+        torch.testing.assert_close(a.float(), b.float(), atol=1e-2 * b.float().abs().max().item(), rtol=0, msg=name)
+    from meepsquared_amd import grouped_linear  # the base product alone (no adapters)
+
+    out = grouped_linear(x.detach(), weight, offsets, is_transposed)
+    want = ref.reference(x.detach(), weight, offsets.cpu(), is_transposed)
+    assert rel(out, want) < BF16_TOL
+
+
 def test_the_product_without_adapters_gives_the_base_and_its_input_gradient():
     from meepsquared_amd import lora_linear
 
@@ -297,14 +323,15 @@ def test_the_fp8_activation_pass_is_bit_exact(K, colscale):
 
 
 @pytest.mark.parametrize("is_transposed", [False, True])
-def test_the_gathered_product_is_bit_identical_to_the_product_of_the_gathered_rows(is_transposed):
+@pytest.mark.parametrize("T", [300, 600])  # 600 tokens: ~300 rows per expert, tall items among them
+def test_the_gathered_product_is_bit_identical_to_the_product_of_the_gathered_rows(is_transposed, T):
     """lora_linear_gathered (rows read through perm, never materialised) against lora_linear on
     hidden[perm // k]: the same tiles and the same sums, so the same bits, gradients included."""
     from meepsquared_amd import _grouped, lora_linear, sort_by_expert
     from meepsquared_amd._moe import _Gather
 
     torch.manual_seed(5)
-    T, k, E, K, N, r = 300, 3, 6, 192, 160, 16
+    k, E, K, N, r = 3, 6, 192, 160, 16
     idx = torch.randint(0, E, (T, k), device="cuda")
     idx[::11, 0] = E  # sentinel ids: rows after every expert
     perm, inv, offsets = sort_by_expert(idx, E)

@@ -146,6 +146,15 @@ def test_qwen3_sized_layer_at_a_quarter_of_the_tokens():
         assert rel(got[name], want[name]) < 1e-2, (name, rel(got[name], want[name]))
 
 
+@pytest.mark.parametrize("is_transposed", [False, True])
+def test_layer_whose_experts_take_tall_items(is_transposed):
+    # 560 tokens, top-4 of 8 experts: rows per expert 262-290 with this seed, so six groups run as one
+    # tall item (257-288 rows) beside two of 289 and 290; the combine's per-row weights ride on them
+    got, want = run_layer(560, 256, 192, 8, 4, 16, 32, is_transposed, seed=11)
+    for name in want:
+        assert rel(got[name], want[name]) < 1e-2, (name, rel(got[name], want[name]))
+
+
 def test_mixtral_shaped_layer_with_zipf_loaded_experts():
     # config 2's routing (E=8, top-2, r=16, Zipf(1.2)-biased logits) at reduced width: the groups are ragged
     got, want = run_layer(1024, 512, 1792, 8, 2, 16, 32, seed=5, zipf=1.2)
