@@ -965,10 +965,8 @@ static_assert(WTile<kWNf4>::RowBytes * 2 == 64, "an NF4 stage is one block of 64
 // larger slots (the small-tile counts included)
 static_assert(STAGES * SlotSize<1, kWBf16, true>::kElems * 2 + BN * 16 * 2 + kSmallLastE * 8 <= 163840,
               "tall items: the slots, the B^T tile and the tile map fit in LDS");
-// (k-contiguous stacks only: the transposing reads of the other orientation need more registers,
-// and its K loop then spills, 22-25 % slower than without tall items)
 template <bool BKC, int NRB, int WT>
-constexpr bool kTallOn = BKC && STAGES == 2 && WT == kWBf16 && NRB <= 1 && WAVES_M == 2 && WAVES_N >= 2 && FN == 2;
+constexpr bool kTallOn = STAGES == 2 && WT == kWBf16 && NRB <= 1 && WAVES_M == 2 && WAVES_N >= 2 && FN == 2;
 
 template <bool BKC, int NRB, int WT, bool TALL = false>
 static int launch_t(const GemmArgs& a, hipStream_t s) {
