@@ -7,6 +7,7 @@ with the Python interface of thinkube/meepsquared's `_grouped` and `_moe` module
 from meepsquared_amd._grouped import (BLOCK_M, RANK_MULTIPLE, Nf4Stack, grouped_linear, lora_linear, max_tiles,
                                       tile_map)
 from meepsquared_amd._moe import Experts, routed_forward, sort_by_expert, topk_softmax
+from meepsquared_amd import _experts as experts  # the Transformers ExpertsInterface implementation
 
 __all__ = ["BLOCK_M", "RANK_MULTIPLE", "Nf4Stack", "grouped_linear", "lora_linear", "max_tiles", "tile_map",
-           "Experts", "routed_forward", "sort_by_expert", "topk_softmax"]
+           "Experts", "routed_forward", "sort_by_expert", "topk_softmax", "experts"]

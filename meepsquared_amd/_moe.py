@@ -238,8 +238,3 @@ def routed_forward(experts, hidden_states, top_k_index, top_k_weights, factors):
         result = _Combine.apply(out, top_k_weights, inv, offsets, k)
     assert result.shape[0] == num_tokens
     return result.to(hidden_states.dtype)
-
-
-def experts_forward(self, hidden_states, top_k_index, top_k_weights):
-    """A Transformers ExpertsInterface-style forward over this module's stacks, without adapters."""
-    return routed_forward(self, hidden_states, top_k_index, top_k_weights, {})

@@ -1,0 +1,105 @@
+"""The routed forward as a Transformers experts implementation, on the GPU: a Qwen3-MoE sparse block
+switched to "meepsquared_amd" against the same block run by Transformers' own eager experts loop in
+float32 (TF:models/qwen3_moe/modeling_qwen3_moe.py:209-281), forward and input gradient; and LoRA
+factors attached to the experts module against the CPU oracle.  Tolerance: relative Frobenius error
+1e-2 (bf16)."""
+
+import copy
+
+import pytest
+import torch
+
+from helpers import rel
+from oracle import moe as ref_moe
+
+pytestmark = pytest.mark.gpu
+transformers = pytest.importorskip("transformers")
+
+
+def tiny_block(E=8, k=2, H=256, I=128, seed=0):
+    from transformers import Qwen3MoeConfig
+    from transformers.models.qwen3_moe.modeling_qwen3_moe import Qwen3MoeSparseMoeBlock
+
+    cfg = Qwen3MoeConfig(hidden_size=H, moe_intermediate_size=I, num_experts=E, num_experts_per_tok=k,
+                         norm_topk_prob=True, hidden_act="silu")
+    torch.manual_seed(seed)
+    block = Qwen3MoeSparseMoeBlock(cfg)
+    with torch.no_grad():
+        block.gate.weight.normal_(0, 0.05)
+        block.experts.gate_up_proj.normal_(0, 0.02)
+        block.experts.down_proj.normal_(0, 0.02)
+    block.experts.gate_up_proj.requires_grad_(False)  # frozen stacks, as in LoRA training
+    block.experts.down_proj.requires_grad_(False)
+    return block, cfg
+
+
+def test_a_qwen3_moe_block_switched_to_the_routed_forward_matches_transformers_eager():
+    from meepsquared_amd import experts
+
+    experts.register()
+    block, cfg = tiny_block()
+    ref_experts = copy.deepcopy(block.experts).float().cuda()  # Transformers' per-expert loop, in float32
+    cfg_ref = copy.deepcopy(cfg)
+    cfg_ref._experts_implementation = "eager"
+    ref_experts.config = cfg_ref
+    block = block.to("cuda", torch.bfloat16)
+    cfg_ours = copy.deepcopy(cfg)
+    cfg_ours._experts_implementation = experts.IMPLEMENTATION
+    block.experts.config = cfg_ours
+    assert experts.routed(block.experts) and not experts.routed(ref_experts)
+
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(2, 96, 256, generator=g).to("cuda", torch.bfloat16)
+    dy = torch.randn(2, 96, 256, generator=g).to("cuda", torch.bfloat16)
+    # the whole sparse block (router + experts) through the routed forward
+    xb = x.clone().requires_grad_()
+    out = block(xb)
+    out.backward(dy)
+    # the same routing into Transformers' eager experts in float32 (a near-tie of the router would
+    # otherwise pick other experts in float32)
+    _, w, idx = block.gate(x.view(-1, 256))
+    w = w.detach()
+    x32 = x.view(-1, 256).float().requires_grad_()
+    out32 = ref_experts(x32, idx, w.float())
+    out32.backward(dy.view(-1, 256).float())
+    # the input gradient through the experts alone (the block's includes the router's part)
+    xe = x.view(-1, 256).clone().requires_grad_()
+    oute = block.experts(xe, idx, w)
+    oute.backward(dy.view(-1, 256))
+    assert torch.equal(out.view(-1, 256), oute.detach())  # the block ran exactly this
+    assert rel(oute, out32) < 1e-2, rel(oute, out32)
+    assert rel(xe.grad, x32.grad) < 1e-2, rel(xe.grad, x32.grad)
+    assert xb.grad is not None and torch.isfinite(xb.grad.float()).all()
+
+
+@pytest.mark.parametrize("k", [2, 8])
+def test_adapters_attached_to_the_experts_module_match_the_oracle(k):
+    from meepsquared_amd import experts, topk_softmax
+
+    experts.register()
+    E, H, I, r, T = 16, 256, 128, 16, 300
+    block, cfg = tiny_block(E=E, k=k, H=H, I=I, seed=2)
+    module = block.experts.to("cuda", torch.bfloat16)
+    cfg._experts_implementation = experts.IMPLEMENTATION
+    module.config = cfg
+    g = torch.Generator().manual_seed(3)
+    f = {"gate_up_proj": ((torch.randn(E, 2 * I, r, generator=g) * 0.05).to("cuda", torch.bfloat16).requires_grad_(),
+                          (torch.randn(E, r, H, generator=g) * 0.05).to("cuda", torch.bfloat16).requires_grad_(), 2.0),
+         "down_proj": ((torch.randn(E, H, r, generator=g) * 0.05).to("cuda", torch.bfloat16).requires_grad_(),
+                       (torch.randn(E, r, I, generator=g) * 0.05).to("cuda", torch.bfloat16).requires_grad_(), 2.0)}
+    experts.set_adapters(module, f)
+    h = torch.randn(T, H, generator=g).to("cuda", torch.bfloat16).requires_grad_()
+    w, idx = topk_softmax(torch.randn(T, E, generator=g).to("cuda", torch.bfloat16), k)
+    out = module(h, idx, w)  # through Qwen3MoeExperts.forward and the ExpertsInterface
+    dy = torch.randn(out.shape, generator=g).to("cuda", torch.bfloat16)
+    out.backward(dy)
+
+    h32 = h.detach().float().requires_grad_()
+    f32 = {n: (a.detach().float().requires_grad_(), b.detach().float().requires_grad_(), s) for n, (a, b, s) in f.items()}
+    o32 = ref_moe.routed_forward(h32, idx, w.float(), module.gate_up_proj.float(), module.down_proj.float(), f32, E)
+    o32.backward(dy.float())
+    assert rel(out, o32) < 1e-2, rel(out, o32)
+    assert rel(h.grad, h32.grad) < 1e-2, rel(h.grad, h32.grad)
+    for n in f:
+        for i in range(2):
+            assert rel(f[n][i].grad, f32[n][i].grad) < 1e-2, (n, i, rel(f[n][i].grad, f32[n][i].grad))
