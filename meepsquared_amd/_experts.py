@@ -120,3 +120,28 @@ def expert_targets(model) -> tuple:
                 names.add(f"{inside_layer.group(1)}.{stack}")
                 stacks += 1
     return sorted(names), stacks
+
+
+def merged_stack(module, name: str, dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+    """A stack with its attached adapter merged, W + scaling * lhs @ rhs for every expert, in the stack's layout.
+
+    As the reference's merged save (src/meepsquared/_save.py:79-95): the factors the training computes
+    with, in float32; an fp8 stack dequantised with its scale first (and an NF4 stack decoded).  A stack
+    without an adapter comes back dequantised.  For saving a merged model; not on the training path.
+    """
+    from meepsquared_amd import _fp8, _grouped, _nf4
+
+    stack = getattr(module, name)
+    if isinstance(stack, _grouped.Nf4Stack):
+        weight = _nf4.dequantize_stack(stack, torch.float32)
+    elif stack.dtype == torch.float8_e4m3fn:
+        weight = _fp8.dequantize_stack(stack.detach(), getattr(module, name + _fp8.STACK_SCALE), torch.float32,
+                                       bool(module.is_transposed))
+    else:
+        weight = stack.detach().float()
+    factors = getattr(module, _FACTORS, {})
+    if name in factors:
+        lhs, rhs, scaling = factors[name]
+        weight = weight + scaling * torch.bmm(lhs.detach().float().contiguous(), rhs.detach().float().contiguous())
+    return weight.to(dtype)
+

@@ -89,3 +89,26 @@ def dequantize_stack(stack: Nf4Stack, dtype: torch.dtype = torch.bfloat16) -> to
     call("mlora_nf4_dequantize", ptr(stack.packed), ptr(stack.absmax_q), ptr(stack.absmax2), ptr(stack.offset),
          ptr(stack.code), ptr(stack.code2), out.numel(), ptr(out), _lib.dtype_code(dtype), _lib.stream(stack.device))
     return out
+
+
+def convert_stacks(experts) -> int:
+    """Every frozen 3-D float stack of an experts module held as NF4 (QLoRA-style); returns how many.
+
+    The NF4 counterpart of `_fp8.convert_stacks` (src/meepsquared/_fp8.py:170-186): the parameter is
+    replaced by an `Nf4Stack` attribute, which the routed forward computes with (decoded in the grouped
+    product).  Stacks already held as NF4 count as converted.
+    """
+    converted = 0
+    for name in list(dict(experts.named_parameters(recurse=False))) + [
+            n for n, v in vars(experts).items() if isinstance(v, Nf4Stack)]:
+        value = getattr(experts, name)
+        if isinstance(value, Nf4Stack):
+            converted += 1
+            continue
+        if value.dim() != 3 or value.requires_grad or not value.is_floating_point():
+            continue
+        stack = quantize_stack(value.detach())
+        delattr(experts, name)  # the parameter goes; the packed stack is a plain attribute
+        setattr(experts, name, stack)
+        converted += 1
+    return converted

@@ -103,3 +103,46 @@ def test_adapters_attached_to_the_experts_module_match_the_oracle(k):
     for n in f:
         for i in range(2):
             assert rel(f[n][i].grad, f32[n][i].grad) < 1e-2, (n, i, rel(f[n][i].grad, f32[n][i].grad))
+
+
+def _module_with_adapters(E=8, H=256, I=128, r=16, seed=4):
+    from meepsquared_amd import experts
+
+    block, cfg = tiny_block(E=E, k=2, H=H, I=I, seed=seed)
+    module = block.experts.to("cuda", torch.bfloat16)
+    cfg._experts_implementation = experts.IMPLEMENTATION
+    module.config = cfg
+    g = torch.Generator().manual_seed(seed + 1)
+    f = {"gate_up_proj": ((torch.randn(E, 2 * I, r, generator=g) * 0.05).to("cuda", torch.bfloat16),
+                          (torch.randn(E, r, H, generator=g) * 0.05).to("cuda", torch.bfloat16), 2.0),
+         "down_proj": ((torch.randn(E, H, r, generator=g) * 0.05).to("cuda", torch.bfloat16),
+                       (torch.randn(E, r, I, generator=g) * 0.05).to("cuda", torch.bfloat16), 2.0)}
+    experts.set_adapters(module, f)
+    return module, g
+
+
+@pytest.mark.parametrize("stacks", ["bf16", "fp8_row", "nf4"])
+def test_merged_stacks_compute_what_the_adapters_add(stacks):
+    """The routed forward with adapters equals the forward on the merged stacks W + s lhs rhs without them
+    (the reference's merged save, src/meepsquared/_save.py:79-95), for bf16, fp8 (per-row scales) and NF4 stacks."""
+    from meepsquared_amd import _fp8, _nf4, experts, topk_softmax
+
+    experts.register()
+    module, g = _module_with_adapters()
+    module.gate_up_proj.requires_grad_(False)
+    module.down_proj.requires_grad_(False)
+    if stacks == "fp8_row":
+        assert _fp8.convert_stacks(module, per_row=True) == 2
+    elif stacks == "nf4":
+        assert _nf4.convert_stacks(module) == 2 and _nf4.convert_stacks(module) == 2  # idempotent
+    T, E = 200, module.num_experts
+    h = torch.randn(T, 256, generator=g).to("cuda", torch.bfloat16)
+    w, idx = topk_softmax(torch.randn(T, E, generator=g).to("cuda", torch.bfloat16), 2)
+    with torch.no_grad():
+        with_adapters = module(h, idx, w)
+        merged = copy.copy(module)
+        merged.gate_up_proj = torch.nn.Parameter(experts.merged_stack(module, "gate_up_proj"), requires_grad=False)
+        merged.down_proj = torch.nn.Parameter(experts.merged_stack(module, "down_proj"), requires_grad=False)
+        experts.set_adapters(merged, {})
+        without = merged(h, idx, w)
+    assert rel(without, with_adapters) < 1e-2, rel(without, with_adapters)
