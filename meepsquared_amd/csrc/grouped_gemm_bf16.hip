@@ -535,7 +535,12 @@ __device__ __forceinline__ void compute(const GemmArgs& p, const bf16* slot, int
     for (int j = 0; j < FN; ++j) nf4_table(code, nf4_absmax(code[16 + nf.q[j]], nf.a2[j], off), tlo[j], thi[j]);
     nf.load(p, kt + 1);
   }
-  if constexpr (AM == 0) f.issue(p, nslot, nkt);
+  // With two slots every wait is for all of a wave's copies, so the stage past the end of K is not
+  // queued at all (the four-slot ring queues zero-filled copies to keep its wait counts constant)
+  const bool queue = STAGES != 2 || nkt * BK < p.K;
+  if constexpr (AM == 0) {
+    if (queue) f.issue(p, nslot, nkt);
+  }
   if constexpr (AM > 0) {
 #pragma unroll
     for (int kk = 0; kk < BK / 16; ++kk) {
@@ -572,9 +577,11 @@ __device__ __forceinline__ void compute(const GemmArgs& p, const bf16* slot, int
       }
       constexpr int last = BK / 16 - 1;
       if (kk <= 2 || kk == last) __builtin_amdgcn_sched_barrier(0);
-      if (kk == 0) f.template issue_part<0>(p, nslot, nkt);
-      if (kk == 1 || (kk == last && last < 1)) f.template issue_part<1>(p, nslot, nkt);
-      if (kk == 2 || (kk == last && last < 2)) f.template issue_part<2>(p, nslot, nkt);
+      if (queue) {
+        if (kk == 0) f.template issue_part<0>(p, nslot, nkt);
+        if (kk == 1 || (kk == last && last < 1)) f.template issue_part<1>(p, nslot, nkt);
+        if (kk == 2 || (kk == last && last < 2)) f.template issue_part<2>(p, nslot, nkt);
+      }
       if (kk <= 2 || kk == last) __builtin_amdgcn_sched_barrier(0);
     }
     if constexpr (NRB > 0) {
@@ -789,7 +796,7 @@ __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_ker
 #endif
       default: kloop<0, BKC, NRB, WT>(p, f, slots, nk, lane, wm, wn, acc, lacc, tacc, tlacc, nf, code, off); break;
     }
-    wait_vm<0>();     // the zero-filled copies queued past the end of K
+    wait_vm<0>();     // (four slots) the zero-filled copies queued past the end of K
     __syncthreads();  // every wave is done with the ring (all copies waited for in the loop)
 
     // ---- epilogue ----
