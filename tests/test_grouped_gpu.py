@@ -151,6 +151,44 @@ def test_tall_items_match_one_product_per_expert(is_transposed):
     assert rel(out, want) < BF16_TOL
 
 
+@pytest.mark.parametrize("seed", range(6))
+def test_random_groups_around_the_tile_boundaries_match_the_oracle(seed):
+    """Seeded sweep: group sizes drawn around every tile boundary (0, 1, 31-33, 255-257, 287-289, 511-513,
+    543-545 rows), random K and N (multiples of 8), both stack layouts, rank 0 / 8 / 16 / 32, with or
+    without a bias; output and all gradients against the oracle."""
+    g = torch.Generator().manual_seed(100 + seed)
+    pick = lambda xs: xs[int(torch.randint(len(xs), (1,), generator=g))]
+    sizes = [0, 1, 31, 32, 33, 255, 256, 257, 287, 288, 289, 511, 512, 513, 543, 544, 545, 600]
+    experts = int(torch.randint(2, 9, (1,), generator=g))
+    rows_per_expert = [pick(sizes) for _ in range(experts)]
+    K, N = 8 * int(torch.randint(4, 40, (1,), generator=g)), 8 * int(torch.randint(4, 72, (1,), generator=g))
+    rank, is_transposed, with_bias = pick([0, 8, 16, 32]), bool(seed % 2), seed % 3 != 0
+    torch.manual_seed(seed)
+    offsets = offsets_of(rows_per_expert)
+    x = torch.randn(sum(rows_per_expert) + 5, K, device="cuda", dtype=torch.bfloat16)  # 5 rows past the last expert
+    shape = (experts, K, N) if is_transposed else (experts, N, K)
+    weight = torch.randn(shape, device="cuda", dtype=torch.bfloat16) * 0.05
+    bias = torch.randn(experts, N, device="cuda", dtype=torch.bfloat16) if with_bias else None
+    live = int(offsets[-1])
+    case = (rows_per_expert, K, N, rank, is_transposed, with_bias)
+    if rank == 0:
+        from meepsquared_amd import grouped_linear
+
+        out = grouped_linear(x, weight, offsets, is_transposed)
+        want = ref.reference(x[:live], weight, offsets.cpu(), is_transposed)
+        if live:
+            assert rel(out[:live], want) < BF16_TOL, case
+        return
+    x = x[:live].clone().requires_grad_()
+    lhs, rhs = adapters(experts, K, N, rank, is_transposed)
+    got, expected = run_both(x, weight, None, offsets, is_transposed, lhs, rhs, 2.0, bias)
+    for name, a, b in zip(("out", "grad_x", "grad_lhs", "grad_rhs"), got, expected):
+        if b.float().norm() == 0:
+            assert a.float().abs().max() == 0, (name, case)
+            continue
+        assert rel(a, b) < BF16_TOL, (name, rel(a, b), case)
+
+
 def test_the_product_without_adapters_gives_the_base_and_its_input_gradient():
     from meepsquared_amd import lora_linear
 
