@@ -590,6 +590,7 @@ static int grouped_gemm_impl(const void* x, int64_t ldx, const int64_t* gather, 
   if (gather != nullptr) {
     if (w_dtype != MLORA_DT_BF16) return fail("grouped_gemm_gather: gathered rows need a bf16 stack");
     if (gk < 1) return fail("grouped_gemm_gather: k=%d must be >= 1", gk);
+    if (rows > (int64_t)0xFFFFFFFFu) return fail("grouped_gemm_gather: rows=%lld must be below 2^32", (long long)rows);
     if (xrows < 0 || xrows * ldx * 2 > 0x7FFFFFF0) return fail("grouped_gemm_gather: x (%lld rows) exceeds 2 GiB", (long long)xrows);
   }
   if (row_scale != nullptr) {

@@ -253,7 +253,8 @@ struct Feed {
       if (p.gather == nullptr) {
         xo[q] = (uint32_t)((row * p.ldx + c * 8) * 2);
       } else {  // the row's source row of x (x's resource spans all of x)
-        const int64_t src = row < mrows ? p.gather[row0 + row] / p.gk : -1;
+        // (32-bit division: the routed rows number below 2^32, checked at the ABI)
+        const int64_t src = row < mrows ? (int64_t)((uint32_t)p.gather[row0 + row] / (uint32_t)p.gk) : -1;
         xo[q] = src >= 0 ? (uint32_t)((src * p.ldx + c * 8) * 2) : kOob;
       }
       xk[q] = c * 8;
@@ -289,7 +290,7 @@ struct Feed {
       if (p.gather == nullptr) {
         to = (uint32_t)(((BM + row) * p.ldx + c * 8) * 2);  // rows past the item: past its resource, zeros
       } else {
-        const int64_t src = BM + row < mrows ? p.gather[row0 + BM + row] / p.gk : -1;
+        const int64_t src = BM + row < mrows ? (int64_t)((uint32_t)p.gather[row0 + BM + row] / (uint32_t)p.gk) : -1;
         to = src >= 0 ? (uint32_t)((src * p.ldx + c * 8) * 2) : kOob;
       }
       tk = c * 8;
