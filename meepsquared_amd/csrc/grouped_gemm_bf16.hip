@@ -23,6 +23,8 @@
 // Waves are WAVES_M x WAVES_N; wave (wm, wn) owns the interleaved 32-row blocks i*WAVES_M + wm and
 // 32-column blocks j*WAVES_N + wn; the K loop is specialised on the number of its row blocks that
 // hold rows of the expert (the last tile of an expert is usually partial), with no branch inside.
+// An expert's last tile of at most XR rows past a full one is merged into it (a "tall" item, the
+// TALL instantiation): each wave then also multiplies the extra rows by its column block wm*WAVES_N+wn.
 //
 // Reference behaviour: src/meepsquared/_grouped.py:120-221 (_grouped_gemm_kernel), :313-345 (_launch).
 #include <mutex>
