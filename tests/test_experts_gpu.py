@@ -146,3 +146,42 @@ def test_merged_stacks_compute_what_the_adapters_add(stacks):
         experts.set_adapters(merged, {})
         without = merged(h, idx, w)
     assert rel(without, with_adapters) < 1e-2, rel(without, with_adapters)
+
+
+def test_a_qwen3_moe_causal_lm_switched_to_the_routed_forward_matches_the_eager_one():
+    """A whole (tiny, one-layer) Qwen3-MoE causal LM in bf16: the same model with Transformers' eager experts
+    and with experts.use(model) gives the same logits and embedding gradient to bf16 tolerance (one MoE layer,
+    so both runs route the same tokens to the same experts); the stacks are frozen as in LoRA training."""
+    from transformers import Qwen3MoeConfig, Qwen3MoeForCausalLM
+
+    from meepsquared_amd import experts
+
+    cfg = Qwen3MoeConfig(vocab_size=128, hidden_size=256, intermediate_size=512, moe_intermediate_size=128,
+                         num_hidden_layers=1, num_attention_heads=4, num_key_value_heads=2, head_dim=64,
+                         num_experts=8, num_experts_per_tok=2, norm_topk_prob=True)
+    torch.manual_seed(0)
+    model = Qwen3MoeForCausalLM(cfg)
+    with torch.no_grad():
+        for name, prm in model.named_parameters():
+            if prm.dim() > 1:
+                prm.normal_(0, 0.05)
+    for name, prm in model.named_parameters():
+        if name.endswith("experts.gate_up_proj") or name.endswith("experts.down_proj"):
+            prm.requires_grad_(False)
+    model = model.to("cuda", torch.bfloat16)
+    ours = copy.deepcopy(model)
+    model.set_experts_implementation("eager")
+    assert experts.use(ours) == 1
+    ids = torch.randint(0, 128, (2, 80), generator=torch.Generator().manual_seed(1)).cuda()
+
+    def run(m):
+        m.zero_grad(set_to_none=True)
+        out = m(input_ids=ids, labels=ids)
+        out.loss.backward()
+        return out.logits.detach().float(), m.model.embed_tokens.weight.grad.float(), out.loss.item()
+
+    logits_e, grad_e, loss_e = run(model)
+    logits_o, grad_o, loss_o = run(ours)
+    assert rel(logits_o, logits_e) < 1e-2, rel(logits_o, logits_e)
+    assert rel(grad_o, grad_e) < 2e-2, rel(grad_o, grad_e)
+    assert abs(loss_o - loss_e) < 1e-2 * abs(loss_e), (loss_o, loss_e)
