@@ -129,8 +129,8 @@ int mlora_grouped_gemm(const void* x, int64_t ldx, int64_t rows, int K, int N,
  * output row r is (c · x W + scaling · bf16(x A) B) · row_scale[gather[r]] + bias: the input gradient
  * of the down product straight from the layer's output gradient, the combine weights applied per row
  * (src/meepsquared/_moe.py:123-126 and the down projection's backward, without the weighted copy of
- * the gradient); low stays bf16(x A) of the unscaled rows.  bf16 stacks only; the other arguments
- * as mlora_grouped_gemm's (no per-row stack scale along k). */
+ * the gradient); low stays bf16(x A) of the unscaled rows.  bf16 stacks only; rows < 2^32; the other
+ * arguments as mlora_grouped_gemm's (no per-row stack scale along k). */
 int mlora_grouped_gemm_gather(const void* x, int64_t ldx, int64_t x_rows, const int64_t* gather, int k,
                               const void* row_scale, int row_scale_dtype, int64_t rows,
                               int K, int N, const void* w, int w_dtype, int64_t w_se, int64_t w_sk, int64_t w_sn,
@@ -142,7 +142,8 @@ int mlora_grouped_gemm_gather(const void* x, int64_t ldx, int64_t x_rows, const 
 
 /* out[e, n, r] = bf16(scaling · sum over expert e's rows of g[row, n] · l[row, r]), fp32
  * accumulation in a fixed order, no atomics: the adapters' gradients.  g (rows, N) bf16 row stride
- * ldg; l (rows, R) bf16 row stride ldl; out addressed out[e*o_se + n*o_sn + r*o_sr].  R <= 64.
+ * ldg; l (rows, R) bf16 row stride ldl; out addressed out[e*o_se + n*o_sn + r*o_sr].  R <= 64,
+ * rows < 2^32.
  * Replaces _grouped_reduce_kernel (src/meepsquared/_grouped.py:232-256). */
 int mlora_grouped_reduce(const void* g, int64_t ldg, const void* l, int64_t ldl, int64_t rows, int N, int R,
                          float scaling, const int32_t* offsets, int E,
