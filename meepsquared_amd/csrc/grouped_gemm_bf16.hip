@@ -569,6 +569,9 @@ __device__ __forceinline__ void compute(const GemmArgs& p, const bf16* slot, int
           bfr[j] = w_frag<BKC, WT>(bs, (j * WAVES_N + wn) * 32, kk, lane);
         }
       }
+      // the step's MFMAs at raised wave priority: of the two waves on a SIMD, the one with MFMAs ready
+      // wins the issue slot over the other's LDS reads and copies (-0.85 % product time)
+      __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int i = 0; i < AM; ++i)
 #pragma unroll
@@ -578,6 +581,7 @@ __device__ __forceinline__ void compute(const GemmArgs& p, const bf16* slot, int
         const bf16x8 at = *(const bf16x8*)(slot + kXOff + swz_rk(lane & 31, kk * 2 + (lane >> 5)));
         tacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wm == 0 ? bfr[0] : bfr[1], at, tacc, 0, 0, 0);
       }
+      __builtin_amdgcn_s_setprio(0);
       constexpr int last = BK / 16 - 1;
       if (kk <= 2 || kk == last) __builtin_amdgcn_sched_barrier(0);
       if (queue) {
