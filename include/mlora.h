@@ -59,8 +59,11 @@ const char* mlora_last_error(void);
  * Routing
  * ------------------------------------------------------------------------------------------- */
 
-/* Router: probs = softmax(logits, fp32) over E, the k largest (descending; equal values in
- * ascending expert order), weights = probs (renorm=0) or probs / sum of the k (renorm=1), cast to
+/* Router: probs = softmax(logits, fp32) over E, the k largest in the order torch.topk returns them
+ * on the GPU, ties included (equal probabilities at the k-th place taken in ascending expert order;
+ * for k <= 32 the k sorted descending by torch's 32-wide bitonic network, which places equal values
+ * in an order of its own; for k > 32 equal values in ascending expert order), weights = probs
+ * (renorm=0) or probs / sum of the k (renorm=1), cast to
  * w_dtype (MLORA_DT_BF16 or MLORA_DT_F32).  logits: (T, E) of logits_dtype (bf16/f16/f32) with
  * row stride ld_logits; out_idx (T, k) int64; out_w (T, k).  E <= 1024, 1 <= k <= min(E, 64).
  * Replaces TF:models/qwen3_moe/modeling_qwen3_moe.py:262-266 (Mixtral: TF:models/mixtral/

@@ -152,8 +152,11 @@ def _transposed(t: torch.Tensor) -> torch.Tensor:
     return out
 
 
-def _scale_args(scale, weight, backward: bool):
-    """(scale, kind, stride_e, on_k): one scale per expert (E,) or per output row (E, out)."""
+def _scale_args(scale, weight, backward: bool, is_transposed: bool):
+    """(scale, kind, stride_e, on_k): one scale per expert (E,) or per output row (E, out) of the stack.
+
+    is_transposed is the layout the launch reads the stack in; in the input-gradient pass (backward)
+    that is the other one, and the stack's output rows run along k."""
     if scale is None:
         return None, _lib.SCALE_NONE, 0, 0
     _lib.require_gpu(scale)
@@ -162,9 +165,12 @@ def _scale_args(scale, weight, backward: bool):
         if scale.numel() != weight.shape[0]:
             raise ValueError(f"a per-expert scale needs {weight.shape[0]} values, got {scale.numel()}")
         return scale, _lib.SCALE_EXPERT, 0, 0
-    if scale.dim() == 2 and scale.shape[0] == weight.shape[0]:
+    stack_transposed = is_transposed != backward  # the stack's own layout: (E, in, out) when True
+    out_rows = weight.shape[2] if stack_transposed else weight.shape[1]
+    if scale.dim() == 2 and tuple(scale.shape) == (weight.shape[0], out_rows):
         return scale, _lib.SCALE_ROW, scale.stride(0), int(backward)
-    raise ValueError(f"scale of shape {tuple(scale.shape)} is neither (experts,) nor (experts, out)")
+    raise ValueError(f"scale of shape {tuple(scale.shape)} is neither ({weight.shape[0]},) per expert nor "
+                     f"({weight.shape[0]}, {out_rows}) per output row of the stack")
 
 
 def _launch(x, weight, scale, offsets, is_transposed, adapters, scaling, bias, store_low, backward=False,
@@ -187,7 +193,7 @@ def _launch(x, weight, scale, offsets, is_transposed, adapters, scaling, bias, s
         return out, low
     offsets = offsets if offsets.dtype == torch.int32 else offsets.to(torch.int32)
     offsets = offsets.contiguous()
-    scale, scale_kind, scale_se, scale_on_k = _scale_args(scale, weight, backward)
+    scale, scale_kind, scale_se, scale_on_k = _scale_args(scale, weight, backward, is_transposed)
     nf4 = (None,) * 5
     if isinstance(weight, Nf4Stack) and w_sk != 1:
         # read with n contiguous (blocks along n): the stack's transposed codes and absmax table, kept on it
@@ -294,7 +300,7 @@ def _launch_fp8(x, weight, scale, offsets, is_transposed, adapters, scaling, bia
     offsets = offsets if offsets.dtype == torch.int32 else offsets.to(torch.int32)
     offsets = offsets.contiguous()
     _lib.require_gpu(weight)
-    scale, scale_kind, scale_se, scale_on_k = _scale_args(scale, weight, backward)
+    scale, scale_kind, scale_se, scale_on_k = _scale_args(scale, weight, backward, is_transposed)
     colscale, cs_se = None, 0
     if scale_kind == _lib.SCALE_ROW and scale_on_k:  # a per-row stack scale along k: folded into x
         colscale, cs_se, scale, scale_kind, scale_se = scale, scale_se, None, _lib.SCALE_NONE, 0
@@ -415,6 +421,9 @@ def _launch_gathered(src, perm, k, weight, scale, offsets, is_transposed, adapte
     """One launch of the product over the rows src[perm // k] (bf16 stack): (out, low).  row_scale:
     output row r multiplied by row_scale[perm[r]] (low stays bf16 of the unscaled rows' x·A)."""
     _lib.require_gpu(src, perm, offsets, weight)
+    if not (isinstance(weight, torch.Tensor) and weight.dtype == torch.bfloat16):
+        raise TypeError(f"the gathered product takes a bf16 stack, not {getattr(weight, 'dtype', type(weight))}: "
+                        "use lora_linear")
     src = src if src.stride(-1) == 1 and src.stride(0) % 8 == 0 and src.data_ptr() % 16 == 0 else src.contiguous()
     T, K = src.shape
     rows = perm.numel()
@@ -424,7 +433,10 @@ def _launch_gathered(src, perm, k, weight, scale, offsets, is_transposed, adapte
     low = torch.empty((rows, R), device=src.device, dtype=torch.bfloat16) if adapters is not None else None
     if rows == 0:
         return out, low
-    scale_, scale_kind, scale_se, _ = _scale_args(scale, weight, backward)
+    scale_, scale_kind, scale_se, on_k = _scale_args(scale, weight, backward, is_transposed)
+    if on_k:  # the gathered kernel applies a per-row stack scale only along n
+        raise ValueError("the gathered product takes no per-output-row stack scale in the input-gradient pass: "
+                         "use lora_linear")
     if bias is not None:
         bias = bias.to(torch.bfloat16)
         bias = bias if bias.stride(-1) == 1 else bias.contiguous()

@@ -28,8 +28,10 @@ def topk_softmax(router_logits: torch.Tensor, top_k: int, renormalize: bool = Tr
     """(top_k_weights, top_k_index) of the router: softmax in fp32, the k largest, optionally renormalised.
 
     As TF:models/qwen3_moe/modeling_qwen3_moe.py:262-266 (weights cast to the logits' dtype) and
-    TF:models/mixtral/modeling_mixtral.py:104-111 (weights_dtype=torch.float32).  Equal
-    probabilities are taken in ascending expert order; indices are int64.
+    TF:models/mixtral/modeling_mixtral.py:104-111 (weights_dtype=torch.float32).  The indices are
+    those torch.topk gives on the GPU, ties included: equal probabilities at the k-th place are taken
+    in ascending expert order, and the k come in torch's order (for k <= 32 that of its bitonic sort,
+    which places equal values in an order of its own); int64.
     """
     _lib.require_gpu(router_logits)
     logits = router_logits.reshape(-1, router_logits.shape[-1])
@@ -186,13 +188,46 @@ def _stack_scale(experts, name):
     return None
 
 
+def _is_silu(act_fn) -> bool:
+    return isinstance(act_fn, torch.nn.SiLU) or type(act_fn).__name__ in ("SiLU", "SiLUActivation")
+
+
+def gate_of(experts):
+    """None when the experts' gate is silu(first half) · second half — the SwiGLU the kernels fuse — else
+    the callable that maps a gate_up output (S, 2I) to the activation (S, I) with PyTorch operations.
+
+    The reference calls `experts._apply_gate` (src/meepsquared/_moe.py:118-119), which Transformers sets
+    to `_default_apply_gate` (chunk, `act_fn(gate) * up`, TF:integrations/moe.py:509-520) unless the
+    experts class defines its own: gpt-oss interleaves gate and up columns, clamps both and gates with
+    `(up + 1) · gate · sigmoid(1.702 · gate)`; DeepSeek-V4 clamps.  Those, and a default gate whose act_fn
+    is not SiLU, take the model's own gate function.
+    """
+    apply_gate = getattr(type(experts), "_apply_gate", None)
+    default = apply_gate is None
+    if apply_gate is not None:
+        try:
+            from transformers.integrations.moe import _default_apply_gate
+        except ImportError:
+            _default_apply_gate = None
+        default = apply_gate is _default_apply_gate
+    act_fn = getattr(experts, "act_fn", None)
+    if default and (act_fn is None or _is_silu(act_fn)):
+        return None
+    if apply_gate is not None:
+        return experts._apply_gate
+
+    def gate(gate_up):
+        g, u = gate_up.chunk(2, dim=-1)
+        return act_fn(g) * u
+
+    return gate
+
+
 def routed_forward(experts, hidden_states, top_k_index, top_k_weights, factors):
     """The experts' forward with each adapter's change added per projection (src/meepsquared/_moe.py:70-126)."""
     if not getattr(experts, "has_gate", True):
         raise NotImplementedError("experts without a gate (up_proj alone) are not built: the kernels fuse SwiGLU")
-    act_fn = getattr(experts, "act_fn", None)
-    if act_fn is not None and not isinstance(act_fn, torch.nn.SiLU) and type(act_fn).__name__ not in ("SiLU", "SiLUActivation"):
-        raise NotImplementedError(f"the gate activation {type(act_fn).__name__}: the kernels compute SwiGLU (silu)")
+    custom_gate = gate_of(experts)
     num_tokens = hidden_states.shape[0]
     k = top_k_index.shape[-1]
     perm, inv, offsets = sort_by_expert(top_k_index, experts.num_experts)
@@ -214,7 +249,7 @@ def routed_forward(experts, hidden_states, top_k_index, top_k_weights, factors):
     else:
         gate_up = project(_Gather.apply(hidden_states, perm, inv, offsets, k), "gate_up_proj", "gate_up_proj_bias")
     down_bias = getattr(experts, "has_bias", False) and experts.down_proj_bias is not None
-    if _grouped.gathered_product_fits(experts.down_proj) and not down_bias:
+    if custom_gate is None and _grouped.gathered_product_fits(experts.down_proj) and not down_bias:
         # SwiGLU, the down product and the combine as one Function: its backward reads the output
         # gradient through perm, and the SwiGLU backward applies the combine weights and forms their
         # gradient (y is not kept)
@@ -224,7 +259,10 @@ def routed_forward(experts, hidden_states, top_k_index, top_k_weights, factors):
                                                       experts.is_transposed, lhs, rhs, scaling)
         assert result.shape[0] == num_tokens
         return result.to(hidden_states.dtype)
-    act = _SwiGLU.apply(gate_up)
+    # the model's own gate (autograd through its PyTorch operations on the GPU), or the SwiGLU kernel
+    act = custom_gate(gate_up) if custom_gate is not None else _SwiGLU.apply(gate_up)
+    if act.dtype != gate_up.dtype:
+        act = act.to(gate_up.dtype)
     if _grouped.gathered_product_fits(experts.down_proj):
         # the down product and the combine as one Function: its backward reads the output gradient
         # through perm, the combine weights applied per row, instead of a weighted copy of it

@@ -76,70 +76,183 @@ __device__ __forceinline__ uint64_t group_max_key(uint64_t v) {
 
 constexpr int kTopkMaxE = 1024;
 
+// torch.topk on the GPU returns the k selected values sorted by a bitonic network over 32 positions
+// when k <= 32 (the k values in expert order — those above the k-th value first, then those equal to
+// it — then empty positions); its comparator swaps a pair when "a above b and a present, or b empty"
+// equals the comparator's direction flag, so equal values change places whenever a comparator with
+// flag false meets them.  Reproduced here so the indices are those torch gives, ties included.
+// Entries are codes rank << 8 | list position (rank: the first selection round that took this value,
+// so a smaller rank is a larger value); an empty position has rank 0xFF.
+constexpr int kTieNet = 32;
+__device__ __forceinline__ void tie_cmpx(uint32_t& a, uint32_t& b, bool flag) {
+  const uint32_t ra = a >> 8, rb = b >> 8;
+  const bool swap = ra < rb || rb == 0xFFu;  // an empty a has the largest rank, so ra < rb implies a present
+  if (swap == flag) {
+    const uint32_t t = a;
+    a = b;
+    b = t;
+  }
+}
+__device__ __forceinline__ void tie_network(uint32_t (&c)[kTieNet]) {
+#pragma unroll
+  for (int size = 2; size < kTieNet; size *= 2)
+#pragma unroll
+    for (int stride = size / 2; stride > 0; stride /= 2)
+#pragma unroll
+      for (int q = 0; q < kTieNet / 2; ++q) {
+        const int a = 2 * q - (q & (stride - 1));
+        tie_cmpx(c[a], c[a + stride], (q & (size / 2)) != 0);
+      }
+#pragma unroll
+  for (int stride = kTieNet / 2; stride > 0; stride /= 2)
+#pragma unroll
+    for (int q = 0; q < kTieNet / 2; ++q) {
+      const int a = 2 * q - (q & (stride - 1));
+      tie_cmpx(c[a], c[a + stride], false);
+    }
+}
+
 template <typename TL, typename TW, int L, int PL>
 __global__ __launch_bounds__(256) void topk_softmax_kernel(const TL* __restrict__ logits, int64_t ld, int64_t T,
                                                            int E, int k, int renorm, int64_t* __restrict__ out_idx,
                                                            TW* __restrict__ out_w) {
   constexpr int G = kWave / L;  // tokens per wave
+  constexpr int TB = 4 * G;     // tokens per block
+  // the k selected experts per token for the reordering (k <= 32): index, probability, rank, then the
+  // list positions in torch's order
+  __shared__ int s_idx[TB][kTieNet];
+  __shared__ float s_p[TB][kTieNet];
+  __shared__ uint32_t s_code[TB][kTieNet];
   const int lane = threadIdx.x & 63, gl = lane & (L - 1);
+  const int tok = (threadIdx.x >> 6) * G + lane / L;  // this lane's token within the block
   const int64_t t0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * G;
-  if (t0 >= T) return;  // whole waves only: the reductions need every lane of a live wave
+  // waves past T take no part in the work but reach every barrier
+  const bool wave_live = t0 < T;
   const int64_t t = t0 + lane / L;
   const bool live = t < T;
-  const TL* row = logits + (live ? t : 0) * ld;
-  float v[PL];
-  float m = -INFINITY;
-#pragma unroll
-  for (int i = 0; i < PL; ++i) {
-    const int e = gl + L * i;
-    v[i] = (live && e < E) ? load_logit(row + e) : -INFINITY;
-    m = fmaxf(m, v[i]);
-  }
-  m = group_max<L>(m);
-  float z = 0.f;
-  uint64_t key[PL];
-#pragma unroll
-  for (int i = 0; i < PL; ++i) {
-    const int e = gl + L * i;
-    if (e < E) z += expf(v[i] - m);
-    key[i] = e < E ? rank_key(v[i], e) : 0;  // 0: absent or already taken
-  }
-  z = group_sum<L>(z);
-
-  // round j: the largest key left over the token's lanes; lane j % L keeps it in its slot j / L
+  const bool reorder = k >= 2 && k <= kTieNet;
   float sel_sum = 0.f, sp[PL];
-  int si[PL];
+  int si[PL], sr[PL];
 #pragma unroll
   for (int s = 0; s < PL; ++s) {
     sp[s] = 0.f;
     si[s] = 0;
+    sr[s] = 0;
   }
-  for (int j = 0; j < k; ++j) {
-    uint64_t best = 0;
+  if (wave_live) {
+    const TL* row = logits + (live ? t : 0) * ld;
+    float v[PL];
+    float m = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < PL; ++i) best = key[i] > best ? key[i] : best;
-    best = group_max_key<L>(best);
-#pragma unroll
-    for (int i = 0; i < PL; ++i) key[i] = key[i] == best ? 0 : key[i];
-    const int idx = (int)(0xFFFFFFFFu - (uint32_t)best);
-    const float p = expf(key_value(best) - m) / z;
-    sel_sum += p;
-    if (gl == (j & (L - 1))) {
-#pragma unroll
-      for (int s = 0; s < PL; ++s)
-        if (s == j / L) {
-          sp[s] = p;
-          si[s] = idx;
-        }
+    for (int i = 0; i < PL; ++i) {
+      const int e = gl + L * i;
+      v[i] = (live && e < E) ? load_logit(row + e) : -INFINITY;
+      m = fmaxf(m, v[i]);
     }
+    m = group_max<L>(m);
+    float z = 0.f;
+    uint64_t key[PL];
+#pragma unroll
+    for (int i = 0; i < PL; ++i) {
+      const int e = gl + L * i;
+      // keyed on x - max in fp32, the softmax's exponent: equal keys are exactly equal probabilities
+      const float d = v[i] - m;
+      if (e < E) z += expf(d);
+      key[i] = e < E ? rank_key(d, e) : 0;  // 0: absent or already taken
+    }
+    z = group_sum<L>(z);
+
+    // round j: the largest key left over the token's lanes; lane j % L keeps it in its slot j / L,
+    // with its rank (the first round that took an equal value)
+    uint32_t prev = 0;
+    int rank = 0;
+    for (int j = 0; j < k; ++j) {
+      uint64_t best = 0;
+#pragma unroll
+      for (int i = 0; i < PL; ++i) best = key[i] > best ? key[i] : best;
+      best = group_max_key<L>(best);
+#pragma unroll
+      for (int i = 0; i < PL; ++i) key[i] = key[i] == best ? 0 : key[i];
+      const uint32_t ord = (uint32_t)(best >> 32);
+      if (j == 0 || ord != prev) rank = j;
+      prev = ord;
+      const int idx = (int)(0xFFFFFFFFu - (uint32_t)best);
+      const float p = expf(key_value(best)) / z;
+      sel_sum += p;
+      if (gl == (j & (L - 1))) {
+#pragma unroll
+        for (int s = 0; s < PL; ++s)
+          if (s == j / L) {
+            sp[s] = p;
+            si[s] = idx;
+            sr[s] = rank;
+          }
+      }
+    }
+    if (reorder) {
+#pragma unroll
+      for (int s = 0; s < PL; ++s) {
+        const int j = s * L + gl;
+        if (j < k) {
+          s_idx[tok][j] = si[s];
+          s_p[tok][j] = sp[s];
+          s_code[tok][j] = (uint32_t)sr[s];
+        }
+      }
+    }
+  }
+  if (reorder) {
+    __syncthreads();
+    // each selection's place in expert order: those above the k-th value by expert index, then those
+    // equal to it (already in expert order, at the end of the list)
+    int gpos[PL];
+    if (wave_live) {
+      const int rk = (int)s_code[tok][k - 1];
+#pragma unroll
+      for (int s = 0; s < PL; ++s) {
+        const int j = s * L + gl;
+        gpos[s] = j;
+        if (j < k && sr[s] != rk) {
+          int below = 0;
+          for (int i = 0; i < rk; ++i) below += s_idx[tok][i] < si[s];
+          gpos[s] = below;
+        }
+      }
+    }
+    __syncthreads();
+    if (wave_live) {
+#pragma unroll
+      for (int s = 0; s < PL; ++s) {
+        const int j = s * L + gl;
+        if (j < k) s_code[tok][gpos[s]] = ((uint32_t)sr[s] << 8) | (uint32_t)j;
+      }
+    }
+    __syncthreads();
+    if (wave_live && gl == 0) {
+      uint32_t c[kTieNet];
+#pragma unroll
+      for (int q = 0; q < kTieNet; ++q) c[q] = q < k ? s_code[tok][q] : 0xFFFFu;
+      tie_network(c);
+#pragma unroll
+      for (int q = 0; q < kTieNet; ++q)
+        if (q < k) s_code[tok][q] = c[q] & 0xFFu;  // output q takes list position c[q] & 0xFF
+    }
+    __syncthreads();
   }
   if (live) {
 #pragma unroll
     for (int s = 0; s < PL; ++s) {
       const int j = s * L + gl;
       if (j < k) {
-        out_idx[t * k + j] = si[s];
-        out_w[t * k + j] = (TW)(renorm ? sp[s] / sel_sum : sp[s]);
+        int ix = si[s];
+        float p = sp[s];
+        if (reorder) {
+          const int from = (int)s_code[tok][j];
+          ix = s_idx[tok][from];
+          p = s_p[tok][from];
+        }
+        out_idx[t * k + j] = ix;
+        out_w[t * k + j] = (TW)(renorm ? p / sel_sum : p);
       }
     }
   }
@@ -450,20 +563,11 @@ extern "C" size_t mlora_route_sort_workspace_bytes(int64_t S, int E) {
   return (size_t)nch * (size_t)(E + 1) * sizeof(int32_t);
 }
 
-extern "C" int mlora_route_sort(const int64_t* ids, int64_t S, int E, int64_t* perm, int64_t* inv, int32_t* offsets,
-                                int block_m, int32_t* tile_expert, int32_t* tile_row, int32_t* tiles,
-                                int64_t max_tiles, void* workspace, size_t workspace_bytes, void* stream) {
-  clear_error();
-  if (S < 0 || S >= ((int64_t)1 << 31)) return fail("route_sort: S=%lld outside [0, 2^31)", (long long)S);
-  if (E < 1 || E > 2048) return fail("route_sort: E=%d outside [1, 2048]", E);
-  if (tile_expert != nullptr && (block_m < 1 || tile_row == nullptr || tiles == nullptr || max_tiles < 0))
-    return fail("route_sort: the tile map needs block_m >= 1, tile_row, tiles and max_tiles >= 0");
-  const size_t need = mlora_route_sort_workspace_bytes(S, E);
-  if (workspace == nullptr || workspace_bytes < need)
-    return fail("route_sort: workspace of %zu bytes, %zu needed", workspace_bytes, need);
-  hipStream_t s = as_stream(stream);
+// The sort proper, on the caller's workspace ws (need bytes, checked by the entry points).
+static int route_sort(const int64_t* ids, int64_t S, int E, int64_t* perm, int64_t* inv, int32_t* offsets,
+                      int block_m, int32_t* tile_expert, int32_t* tile_row, int32_t* tiles, int64_t max_tiles,
+                      int32_t* ws, hipStream_t s) {
   const int nch = (int)(S > 0 ? (S + kSortChunk - 1) / kSortChunk : 0);
-  int32_t* ws = (int32_t*)workspace;
   const int nbits = nbits_for(E);
   const size_t sh_bins = (size_t)(E + 1) * sizeof(int);
   if (nch > 0) {
@@ -479,6 +583,27 @@ extern "C" int mlora_route_sort(const int64_t* ids, int64_t S, int E, int64_t* p
     if (int rc = launch_status("route_sort/scatter")) return rc;
   }
   return 0;
+}
+
+static int route_sort_check(int64_t S, int E, int block_m, const int32_t* tile_expert, const int32_t* tile_row,
+                            const int32_t* tiles, int64_t max_tiles) {
+  if (S < 0 || S >= ((int64_t)1 << 31)) return fail("route_sort: S=%lld outside [0, 2^31)", (long long)S);
+  if (E < 1 || E > 2048) return fail("route_sort: E=%d outside [1, 2048]", E);
+  if (tile_expert != nullptr && (block_m < 1 || tile_row == nullptr || tiles == nullptr || max_tiles < 0))
+    return fail("route_sort: the tile map needs block_m >= 1, tile_row, tiles and max_tiles >= 0");
+  return 0;
+}
+
+extern "C" int mlora_route_sort(const int64_t* ids, int64_t S, int E, int64_t* perm, int64_t* inv, int32_t* offsets,
+                                int block_m, int32_t* tile_expert, int32_t* tile_row, int32_t* tiles,
+                                int64_t max_tiles, void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  if (int rc = route_sort_check(S, E, block_m, tile_expert, tile_row, tiles, max_tiles)) return rc;
+  const size_t need = mlora_route_sort_workspace_bytes(S, E);
+  if (workspace == nullptr || workspace_bytes < need)
+    return fail("route_sort: workspace of %zu bytes, %zu needed", workspace_bytes, need);
+  return route_sort(ids, S, E, perm, inv, offsets, block_m, tile_expert, tile_row, tiles, max_tiles,
+                    (int32_t*)workspace, as_stream(stream));
 }
 
 extern "C" int mlora_tile_map(const int32_t* offsets, int E, int64_t rows, int block_m, int32_t* tile_expert,

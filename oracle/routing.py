@@ -6,21 +6,82 @@ TEST INFRASTRUCTURE ONLY (see oracle/__init__.py).
 import numpy as np
 
 
+BITONIC_WIDTH = 32  # torch sorts the k selected values of a row with a 32-wide bitonic network when k <= 32
+
+
+def _bitonic_stages(width):
+    """The compare-exchange stages of a bitonic sort of `width` (a power of two) positions: per stage the
+    pairs (a, b = a + stride) and each pair's direction flag, as a network of width / 2 comparators
+    (comparator t at a = 2t - (t mod stride)); merges of growing size, then one descending merge of all."""
+    stages = []
+    size = 2
+    while size < width:
+        stride = size // 2
+        while stride:
+            t = np.arange(width // 2)
+            stages.append((2 * t - (t & (stride - 1)), stride, (t & (size // 2)) != 0))
+            stride //= 2
+        size *= 2
+    stride = width // 2
+    while stride:
+        t = np.arange(width // 2)
+        stages.append((2 * t - (t & (stride - 1)), stride, np.zeros(width // 2, dtype=bool)))
+        stride //= 2
+    return stages
+
+
+def _torch_gpu_order(order, key, k):
+    """The k selected experts of each row in the order torch.topk returns them on the GPU.
+
+    torch gathers the selected values in expert order (those strictly above the k-th value first,
+    then those equal to it) and, for k <= 32, sorts them descending with a bitonic network over 32
+    positions (the k values, then empty positions): a comparator swaps its pair when "a above b and a
+    present, or b empty" equals its direction flag, so equal values are exchanged whenever a comparator
+    with flag false meets them.  For k > 32 the sort is stable (equal values stay in expert order).
+    order (T, k): the selected experts, descending, equal values in ascending expert; key: their values.
+    """
+    T = order.shape[0]
+    kth = key[:, k - 1:k]
+    gather = np.argsort(np.where(key > kth, 0, 1) * (1 << 20) + order, axis=1, kind="stable")
+    idx = np.take_along_axis(order, gather, 1)
+    val = np.take_along_axis(key, gather, 1)
+    if k > BITONIC_WIDTH:
+        return order  # a stable descending sort of the expert-ordered values is `order` itself
+    W = BITONIC_WIDTH
+    K = np.zeros((T, W), dtype=np.float64)
+    V = np.zeros((T, W), dtype=np.int64)
+    ok = np.zeros((T, W), dtype=bool)
+    K[:, :k], V[:, :k], ok[:, :k] = val, idx, True
+    for a, stride, flag in _bitonic_stages(W):
+        b = a + stride
+        swap = ((K[:, a] > K[:, b]) & ok[:, a]) | ~ok[:, b]
+        do = swap == flag[None, :]
+        for arr in (K, V, ok):
+            xa, xb = arr[:, a].copy(), arr[:, b].copy()
+            arr[:, a] = np.where(do, xb, xa)
+            arr[:, b] = np.where(do, xa, xb)
+    return V[:, :k]
+
+
 def topk_softmax(logits, k: int, renorm: bool = True):
     """(weights fp32 (T, k), indices int64 (T, k)) of the router.
 
-    Follows TF:models/qwen3_moe/modeling_qwen3_moe.py:262-266: softmax in fp32, the k largest,
-    renormalised over the k when `renorm`.  Order: descending probability; equal logits in
-    ascending expert index (a stable sort of -logit).  Selection is done on the logits, which order
-    the exact softmax probabilities the same way.
-    Pinned by: torch.topk on tie-free inputs (identical indices) and a brute-force sort on inputs
-    with ties (tests/test_oracle.py).
+    Follows TF:models/qwen3_moe/modeling_qwen3_moe.py:262-266: softmax in fp32, torch.topk of the
+    probabilities, renormalised over the k when `renorm`.  Selection and ties follow torch.topk on the
+    GPU, where the reference's router runs: equal probabilities at the k-th place are taken in
+    ascending expert order, and the k are returned in torch's GPU order (_torch_gpu_order).  Equal
+    probabilities are equal values of x - max(x) in fp32, the argument of the softmax's exponential.
+    Pinned by: torch.topk on the GPU over bf16 logits with ties, k = 1 .. 40
+    (tests/golden/topk_gpu.npz, indices bit-exact), torch.topk on tie-free logits (routing.npz), and a
+    brute-force selection on ties (tests/test_oracle.py).
     """
     x = np.asarray(logits, dtype=np.float32)
-    x = x + np.float32(0.0)  # -0.0 and +0.0 are one value
-    order = np.argsort(-x, axis=-1, kind="stable")[:, :k]
     m = x.max(axis=-1, keepdims=True)
-    e = np.exp((x - m).astype(np.float64))
+    d = (x - m).astype(np.float32) + np.float32(0.0)  # -0.0 and +0.0 are one value
+    order = np.argsort(-d, axis=-1, kind="stable")[:, :k]
+    if k > 1:
+        order = _torch_gpu_order(order, np.take_along_axis(d, order, 1).astype(np.float64), k)
+    e = np.exp(d.astype(np.float64))
     p = (e / e.sum(axis=-1, keepdims=True)).astype(np.float32)
     w = np.take_along_axis(p, order, axis=-1)
     if renorm:

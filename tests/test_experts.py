@@ -78,3 +78,27 @@ def test_set_adapters_checks_the_factors_against_the_stack_layout(is_transposed)
         experts.set_adapters(module, {"up_proj": good["gate_up_proj"]})
     with pytest.raises(TypeError):
         experts.set_adapters(torch.nn.Linear(2, 2), good)
+
+
+def test_the_fused_swiglu_is_taken_only_for_the_default_silu_gate():
+    """gate_of: None (the SwiGLU kernel) for Transformers' default gate with SiLU and for this package's
+    Experts container; the model's own gate function for gpt-oss (interleaved, clamped, sigmoid(1.702 g))
+    and for a default gate whose act_fn is not SiLU."""
+    from transformers import GptOssConfig
+    from transformers.models.gpt_oss.modeling_gpt_oss import GptOssExperts
+
+    from meepsquared_amd import Experts
+    from meepsquared_amd._moe import gate_of
+
+    qwen = tiny_qwen3_moe(1).model.layers[0].mlp.experts
+    assert gate_of(qwen) is None
+    assert gate_of(Experts(torch.zeros(2, 8, 4), torch.zeros(2, 4, 4))) is None
+    oss = GptOssExperts(GptOssConfig(hidden_size=16, intermediate_size=8, num_local_experts=2))
+    gate = gate_of(oss)
+    assert gate is not None
+    gu = torch.randn(5, 16)
+    assert torch.equal(gate(gu), oss._apply_gate(gu))
+    qwen.act_fn = torch.nn.GELU()
+    gate = gate_of(qwen)
+    g, u = gu.chunk(2, dim=-1)
+    assert gate is not None and torch.equal(gate(gu), torch.nn.functional.gelu(g) * u)

@@ -185,3 +185,59 @@ def test_a_qwen3_moe_causal_lm_switched_to_the_routed_forward_matches_the_eager_
     assert rel(logits_o, logits_e) < 1e-2, rel(logits_o, logits_e)
     assert rel(grad_o, grad_e) < 2e-2, rel(grad_o, grad_e)
     assert abs(loss_o - loss_e) < 1e-2 * abs(loss_e), (loss_o, loss_e)
+
+
+@pytest.mark.parametrize("with_adapters", [False, True])
+def test_gpt_oss_experts_with_their_own_gate_match_transformers_eager(with_adapters):
+    """GptOssExperts (transposed stacks with biases, interleaved gate/up columns, the clamped
+    (up + 1) · gate · sigmoid(1.702 · gate) gate, TF:models/gpt_oss/modeling_gpt_oss.py:68-113) switched
+    to the routed forward: the products run on the kernels and the gate is the module's own
+    `_apply_gate`, as src/meepsquared/_moe.py:118 calls it.  Against Transformers' eager loop in
+    float32 (with adapters: the eager loop on the merged stacks W + s·lhs@rhs), forward and input
+    gradient, relative error 1e-2."""
+    from transformers import GptOssConfig
+    from transformers.models.gpt_oss.modeling_gpt_oss import GptOssExperts
+
+    from meepsquared_amd import experts, topk_softmax
+
+    experts.register()
+    E, H, I, k, T, r, s = 8, 128, 64, 2, 200, 16, 2.0
+    cfg = GptOssConfig(hidden_size=H, intermediate_size=I, num_local_experts=E, num_experts_per_tok=k)
+    torch.manual_seed(3)
+    module = GptOssExperts(cfg)
+    with torch.no_grad():
+        module.gate_up_proj.normal_(0, 0.1)  # gates reach the clamp at 7 now and then
+        module.gate_up_proj_bias.normal_(0, 0.5)
+        module.down_proj.normal_(0, 0.05)
+        module.down_proj_bias.normal_(0, 0.1)
+    for p in module.parameters():
+        p.requires_grad_(False)
+    ref = copy.deepcopy(module).float().cuda()
+    cfg_ref = copy.deepcopy(cfg)
+    cfg_ref._experts_implementation = "eager"
+    ref.config = cfg_ref
+    module = module.to("cuda", torch.bfloat16)
+    cfg_ours = copy.deepcopy(cfg)
+    cfg_ours._experts_implementation = experts.IMPLEMENTATION
+    module.config = cfg_ours
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn(T, H, generator=g).to("cuda", torch.bfloat16)
+    dy = torch.randn(T, H, generator=g).to("cuda", torch.bfloat16)
+    w, idx = topk_softmax(torch.randn(T, E, generator=g).to("cuda", torch.bfloat16), k)
+    if with_adapters:  # transposed stacks: lhs (E, in, r), rhs (E, r, out)
+        fa = {"gate_up_proj": ((torch.randn(E, H, r, generator=g) * 0.05).to("cuda", torch.bfloat16),
+                               (torch.randn(E, r, 2 * I, generator=g) * 0.05).to("cuda", torch.bfloat16), s),
+              "down_proj": ((torch.randn(E, I, r, generator=g) * 0.05).to("cuda", torch.bfloat16),
+                            (torch.randn(E, r, H, generator=g) * 0.05).to("cuda", torch.bfloat16), s)}
+        experts.set_adapters(module, fa)
+        with torch.no_grad():
+            for name, (lhs, rhs, sc) in fa.items():
+                getattr(ref, name).add_(sc * (lhs.float() @ rhs.float()))
+    xb = x.clone().requires_grad_()
+    out = module(xb, idx, w)
+    out.backward(dy)
+    x32 = x.float().requires_grad_()
+    out32 = ref(x32, idx, w.float())
+    out32.backward(dy.float())
+    assert rel(out, out32) < 1e-2, rel(out, out32)
+    assert rel(xb.grad, x32.grad) < 1e-2, rel(xb.grad, x32.grad)

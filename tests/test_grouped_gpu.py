@@ -484,3 +484,41 @@ def test_an_nf4_stack_read_the_other_way_is_bit_identical_to_its_decoded_twin(is
     assert torch.equal(res[0][1], res[1][1])
     if is_transposed:
         assert torch.equal(res[0][0], res[1][0])
+
+
+@pytest.mark.parametrize("is_transposed", [False, True])
+def test_a_scale_of_the_wrong_shape_is_refused(is_transposed):
+    """A per-row scale must be (experts, out rows of the stack): (E, in) or a wrong length is a
+    ValueError naming the shape it needs, forward and backward alike."""
+    from meepsquared_amd import _fp8, lora_linear
+
+    E, K, N = 3, 64, 48
+    w = torch.randn((E, K, N) if is_transposed else (E, N, K), device="cuda") * 0.05
+    stack, scale = _fp8.quantize_stack(w, per_row=True, is_transposed=is_transposed)
+    assert scale.shape == (E, N)
+    x = torch.randn(30, K, device="cuda", dtype=torch.bfloat16)
+    offsets = offsets_of([10, 10, 10])
+    for bad in (torch.ones(E, K, device="cuda"), torch.ones(E, N + 8, device="cuda"), torch.ones(E + 1, device="cuda")):
+        with pytest.raises(ValueError, match=f"\\({E}, {N}\\)|{E} values"):
+            lora_linear(x, stack, bad, offsets, is_transposed, products_fp8=False)
+    lora_linear(x, stack, scale, offsets, is_transposed, products_fp8=False)  # the right shape is taken
+
+
+def test_the_gathered_products_refuse_what_their_kernel_does_not_take():
+    """The gathered product reads bf16 stacks only and applies no per-row stack scale along k: an fp8
+    stack is a TypeError, a per-row scale in the input-gradient pass a ValueError (lora_linear takes both)."""
+    from meepsquared_amd import _fp8, _grouped, sort_by_expert
+
+    E, K, N, k, T = 3, 64, 48, 2, 20
+    idx = torch.randint(0, E, (T, k), device="cuda")
+    perm, inv, offsets = sort_by_expert(idx, E)
+    h = torch.randn(T, K, device="cuda", dtype=torch.bfloat16)
+    w8, s8 = _fp8.quantize_stack(torch.randn(E, N, K, device="cuda") * 0.05, per_row=True)
+    with pytest.raises(TypeError, match="bf16 stack"):
+        _grouped.lora_linear_gathered(h, perm, inv, k, w8, s8, offsets, False)
+    wb = torch.randn(E, N, K, device="cuda", dtype=torch.bfloat16)
+    x = torch.randn(T * k, K, device="cuda", dtype=torch.bfloat16, requires_grad=True)
+    wts = torch.rand(T, k, device="cuda")
+    out = _grouped.lora_linear_combined(x, wts, perm, inv, k, wb, torch.ones(E, N, device="cuda"), offsets, False)
+    with pytest.raises(ValueError, match="per-output-row"):
+        out.backward(torch.ones_like(out))

@@ -49,14 +49,62 @@ def test_router_matches_torch_topk_on_the_golden_logits(golden):
     np.testing.assert_allclose(w, g["topk_w"], rtol=1e-6, atol=1e-7)
 
 
-def test_router_ties_go_to_the_lower_expert():
+def test_router_ties_at_the_kth_place_go_to_the_lower_expert():
+    # brute force: the selected set is the k first of (value descending, expert ascending), returned in
+    # non-increasing order of value (the order among equal values is torch's: pinned by topk_gpu.npz)
     rng = np.random.default_rng(0)
     x = rng.integers(-3, 4, size=(64, 32)).astype(np.float32)  # many ties
-    w, idx = routing.topk_softmax(x, 5)
-    for r in range(64):
-        brute = sorted(range(32), key=lambda e: (-x[r, e], e))[:5]
-        assert idx[r].tolist() == brute
-    np.testing.assert_allclose(w.sum(axis=1), 1.0, rtol=1e-6)
+    for k in (5, 2, 32):
+        w, idx = routing.topk_softmax(x, k)
+        for r in range(64):
+            brute = sorted(range(32), key=lambda e: (-x[r, e], e))[:k]
+            assert sorted(idx[r].tolist()) == sorted(brute)
+            assert np.all(np.diff(x[r, idx[r]]) <= 0)
+        np.testing.assert_allclose(w.sum(axis=1), 1.0, rtol=1e-6)
+
+
+def test_router_order_matches_torch_topk_on_the_gpu_with_ties(golden):
+    """tests/golden/topk_gpu.npz: torch.topk on the GPU over softmax(bf16 logits) with ties inside the k
+    and at its boundary, k = 1 .. 40: the oracle's indices bit-exact, in torch's order."""
+    g = golden("topk_gpu.npz")
+    for c, (T, E, k, seed, q) in enumerate(g["cases"]):
+        x = (g[f"logits_{c}"].astype(np.uint32) << 16).view(np.float32)
+        w, idx = routing.topk_softmax(x, int(k))
+        assert np.array_equal(idx, g[f"idx_{c}"].astype(np.int64)), (c, int(T), int(E), int(k))
+        np.testing.assert_allclose(w, g[f"w_{c}"], rtol=2e-6, atol=1e-7)
+
+
+def test_a_mistake_in_the_tie_network_fails_the_golden(golden, monkeypatch):
+    """The golden pins the order among ties: the network with its direction flags inverted fails it."""
+    g = golden("topk_gpu.npz")
+    stages = routing._bitonic_stages
+
+    def flipped(width):
+        return [(a, stride, ~flag) for a, stride, flag in stages(width)]
+
+    monkeypatch.setattr(routing, "_bitonic_stages", flipped)
+    x = (g["logits_1"].astype(np.uint32) << 16).view(np.float32)
+    _, idx = routing.topk_softmax(x, 8)
+    assert not np.array_equal(idx, g["idx_1"].astype(np.int64))
+
+
+@pytest.mark.parametrize("T,E,k,q", [(4096, 128, 8, 0.0), (2048, 64, 6, 2.0), (4096, 8, 2, 0.0)])
+def test_router_selection_matches_cpu_torch_topk_on_tied_bf16_logits(T, E, k, q):
+    """torch.topk on the CPU (its order among equal values differs from the GPU's and is not pinned
+    here): the probabilities of the oracle's experts are torch's top-k values, position by position,
+    and the selected sets are equal wherever the k-th and (k+1)-th probabilities differ."""
+    g = torch.Generator().manual_seed(T + E + k)
+    logits = torch.randn(T, E, generator=g)
+    if q:
+        logits = (logits * q).round() / q
+    logits = logits.to(torch.bfloat16).float()
+    probs = torch.softmax(logits, dim=-1)
+    vals, tidx = torch.topk(probs, k)
+    _, idx = routing.topk_softmax(logits.numpy(), k)
+    assert torch.equal(probs.gather(1, torch.from_numpy(idx)), vals)
+    srt = probs.sort(dim=1, descending=True).values
+    untied = (srt[:, k - 1] != srt[:, k]).numpy()
+    assert np.array_equal(np.sort(idx[untied], 1), np.sort(tidx.numpy()[untied], 1))
 
 
 def test_router_without_renormalisation_gives_the_softmax_probabilities():

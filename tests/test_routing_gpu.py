@@ -39,6 +39,42 @@ def test_topk_indices_are_bit_exact_with_ties(T, E, k, dtype):
     np.testing.assert_allclose(w.cpu().numpy(), ow, rtol=1e-5, atol=1e-6)
 
 
+def test_topk_matches_the_golden_gpu_torch_topk_with_ties(golden):
+    """tests/golden/topk_gpu.npz (torch.topk on the GPU, bf16 logits with ties, k = 1 .. 40): indices
+    bit-exact, in torch's order; renormalised fp32 weights to the last bits."""
+    from meepsquared_amd import topk_softmax
+
+    g = golden("topk_gpu.npz")
+    for c, (T, E, k, seed, q) in enumerate(g["cases"]):
+        logits = torch.from_numpy(g[f"logits_{c}"].view(np.int16)).view(torch.bfloat16).cuda()
+        w, idx = topk_softmax(logits, int(k), renormalize=True, weights_dtype=torch.float32)
+        assert np.array_equal(idx.cpu().numpy(), g[f"idx_{c}"].astype(np.int64)), (c, int(T), int(E), int(k))
+        np.testing.assert_allclose(w.cpu().numpy(), g[f"w_{c}"], rtol=2e-6, atol=1e-7)
+
+
+@pytest.mark.parametrize("q", [0.0, 4.0])
+@pytest.mark.parametrize("weights_dtype", [torch.bfloat16, torch.float32])
+def test_topk_matches_torch_topk_on_the_same_gpu(q, weights_dtype):
+    """The reference's router on config 1's logits (T=8192, E=128, top-8, bf16 N(0,1), seed 0; q = 4: logits
+    rounded to quarters, ties in most rows), run by torch on this GPU: softmax(fp32) -> topk -> renormalise
+    -> cast (TF:models/qwen3_moe/modeling_qwen3_moe.py:262-266).  Indices bit-exact, ties included;
+    weights within one rounding of the dtype."""
+    from meepsquared_amd import topk_softmax
+
+    g = torch.Generator().manual_seed(0)
+    logits = torch.randn(8192, 128, generator=g)
+    if q:
+        logits = (logits * q).round() / q
+    logits = logits.to(torch.bfloat16).cuda()
+    probs = torch.softmax(logits, dim=-1, dtype=torch.float)
+    vals, tidx = torch.topk(probs, 8, dim=-1)
+    tw = (vals / vals.sum(dim=-1, keepdim=True)).to(weights_dtype)
+    w, idx = topk_softmax(logits, 8, renormalize=True, weights_dtype=weights_dtype)
+    assert torch.equal(idx, tidx)
+    tol = dict(rtol=4e-3, atol=0) if weights_dtype == torch.bfloat16 else dict(rtol=2e-6, atol=1e-7)
+    torch.testing.assert_close(w, tw, **tol)
+
+
 def test_topk_without_renormalisation_and_bf16_weights():
     from meepsquared_amd import topk_softmax
 
