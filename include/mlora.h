@@ -84,6 +84,18 @@ int mlora_route_sort(const int64_t* ids, int64_t S, int E, int64_t* perm, int64_
                      int block_m, int32_t* tile_expert, int32_t* tile_row, int32_t* tiles, int64_t max_tiles,
                      void* workspace, size_t workspace_bytes, void* stream);
 
+/* mlora_route_sort without a workspace argument, for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  No counterpart in
+ * the reference.  The histograms live in a 4 MiB array of the library's own, one per GPU (the device
+ * current on the calling thread), held until the process ends: S and E must satisfy
+ * mlora_route_sort_workspace_bytes(S, E) <= 4194304 (e.g. S <= 2,080,768 ids at E = 128), else the call is
+ * refused.  It calls no hipMalloc or hipFree.  Calls on one GPU share the array: calls that overlap
+ * (concurrent streams) race; calls in sequence on one stream do not.  Results are those of
+ * mlora_route_sort. */
+int mlora_route_sort_noalloc(const int64_t* ids, int64_t S, int E, int64_t* perm, int64_t* inv, int32_t* offsets,
+                             int block_m, int32_t* tile_expert, int32_t* tile_row, int32_t* tiles,
+                             int64_t max_tiles, void* stream);
+
 /* The tile map of src/meepsquared/_grouped.py:88-103: each expert's rows cut into block_m-row
  * tiles; tile_expert/tile_row (max_tiles,) int32, tiles a single int32 (the real count).  Spare
  * entries hold the last expert and the row the reference's formula gives.  E <= 4096. */

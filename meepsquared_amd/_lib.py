@@ -26,6 +26,7 @@ SIGNATURES = {
     "mlora_route_topk": (c_int, [P, c_int, I64, I64, c_int, c_int, c_int, P, P, c_int, P]),
     "mlora_route_sort_workspace_bytes": (c_size_t, [I64, c_int]),
     "mlora_route_sort": (c_int, [P, I64, c_int, P, P, P, c_int, P, P, P, I64, P, c_size_t, P]),
+    "mlora_route_sort_noalloc": (c_int, [P, I64, c_int, P, P, P, c_int, P, P, P, I64, P]),
     "mlora_tile_map": (c_int, [P, c_int, I64, c_int, P, P, P, I64, P]),
     "mlora_grouped_gemm": (c_int, [P, I64, I64, c_int, c_int,
                                    P, c_int, I64, I64, I64,

@@ -6,6 +6,8 @@
 //   router       TF:models/qwen3_moe/modeling_qwen3_moe.py:262-266 — softmax(fp32) -> topk -> renorm
 //   sort/offsets src/meepsquared/_moe.py:77-87 — sort(expert_ids), histc, cumsum(int32), sentinels
 //   tile map     src/meepsquared/_grouped.py:83-103
+#include <mutex>
+
 #include "common.hpp"
 
 namespace mlora {
@@ -604,6 +606,57 @@ extern "C" int mlora_route_sort(const int64_t* ids, int64_t S, int E, int64_t* p
     return fail("route_sort: workspace of %zu bytes, %zu needed", workspace_bytes, need);
   return route_sort(ids, S, E, perm, inv, offsets, block_m, tile_expert, tile_row, tiles, max_tiles,
                     (int32_t*)workspace, as_stream(stream));
+}
+
+// ------------------------------------------------------------------------------------------------
+// The sort for callers that cannot allocate (HIP graph capture, serving loops): the per-chunk
+// histograms live in this array, one per GPU, held until the process ends.  Host code never uses the
+// array's name as an address (on the host it is a stand-in, not device memory): the device address is
+// taken with hipGetSymbolAddress once per device, with that device current, and kept.  The sort writes
+// every entry it later reads, so nothing needs clearing between calls; calls that overlap on one GPU
+// (two streams at once) share the array and race.
+// ------------------------------------------------------------------------------------------------
+constexpr size_t kSortScratchBytes = (size_t)4 << 20;
+static __device__ __align__(256) uint8_t scratch[kSortScratchBytes];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kMaxDevices] = {};
+
+// the scratch array's device address on the current device, or nullptr (the error recorded)
+static int32_t* scratch_on_current_device() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    fail("route_sort_noalloc: no current device (or device index %d past %d)", dev, kMaxDevices - 1);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    const hipError_t err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || ptr == nullptr) {
+      fail("route_sort_noalloc: hipGetSymbolAddress of the scratch array failed on device %d: %s", dev,
+           hipGetErrorString(err));
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = ptr;
+  }
+  return (int32_t*)g_scratch_ptr[dev];
+}
+
+extern "C" int mlora_route_sort_noalloc(const int64_t* ids, int64_t S, int E, int64_t* perm, int64_t* inv,
+                                        int32_t* offsets, int block_m, int32_t* tile_expert, int32_t* tile_row,
+                                        int32_t* tiles, int64_t max_tiles, void* stream) {
+  clear_error();
+  if (int rc = route_sort_check(S, E, block_m, tile_expert, tile_row, tiles, max_tiles)) return rc;
+  const size_t need = mlora_route_sort_workspace_bytes(S, E);
+  if (need > kSortScratchBytes)
+    return fail("route_sort_noalloc: S=%lld ids over E=%d experts need %zu bytes of scratch, past its %zu "
+                "(use mlora_route_sort with a workspace)", (long long)S, E, need, kSortScratchBytes);
+  int32_t* ws = scratch_on_current_device();
+  if (ws == nullptr) return 1;
+  return route_sort(ids, S, E, perm, inv, offsets, block_m, tile_expert, tile_row, tiles, max_tiles, ws,
+                    as_stream(stream));
 }
 
 extern "C" int mlora_tile_map(const int32_t* offsets, int E, int64_t rows, int block_m, int32_t* tile_expert,
