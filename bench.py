@@ -2,7 +2,8 @@
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline]
     python bench.py --copy-calibration MIB    # a plain device copy of known size, for PMC scaling
-    python bench.py --config 3                # config 3: fp8 e4m3 stacks with per-row scales, fp8 MFMA
+    python bench.py --config 3                # config 3: fp8 e4m3 stacks with per-row scales (bf16 products)
+    python bench.py --config 3 --fp8-products # ... with the products on the fp8 MFMA (two e4m3 terms)
     python bench.py --config 2|4              # Mixtral-shaped, Zipf-loaded / packed varlen batch, NF4 stacks
 
 A step is one forward and backward pass of the routed MoE-LoRA layer over one batch of synthetic
@@ -59,7 +60,7 @@ CONFIGS = {
     2: dict(T=16384, H=4096, I=14336, E=8, k=2, r=16, alpha=32, zipf=1.2,
             name="BASELINE config 2: Mixtral-8x7B-shaped MoE-LoRA layer fwd+bwd, Zipf(1.2)-loaded experts"),
     3: dict(T=T, H=H, I=I, E=E, k=K_TOP, r=R, alpha=ALPHA, stack="fp8",
-            name="BASELINE config 3: config 1 with fp8-e4m3 stacks (per-row scales) on the fp8 MFMA"),
+            name="BASELINE config 3: config 1 with fp8-e4m3 stacks (per-row scales)"),
     4: dict(H=H, I=I, E=E, k=K_TOP, r=R, alpha=ALPHA, stack="nf4", varlen=(64, 64, 2048),
             name="BASELINE config 4: config 1 fed from a packed varlen batch (64 sequences, lengths U[64, 2048]), "
                  "NF4 stacks (blocksize 64, double quant)"),
@@ -154,11 +155,12 @@ def read_traffic():
 def roofline(c, achieved, config):
     """The grouped product's achieved rate against the MFMA peak it runs on (traffic measured for config 1)."""
     if c.get("stack") == "fp8" and os.environ.get("MEEPSQUARED_FP8_PRODUCTS") == "0":
-        return {"bound": "mfma", "kernel": "grouped_gemm_bf16_kernel / register-staged kernel, fp8 stacks decoded to bf16",
+        return {"bound": "mfma", "kernel": "grouped_gemm_bf16_kernel, fp8 stacks decoded to bf16 in registers",
                 "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                 "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None}
     if c.get("stack") == "fp8":
-        return {"bound": "mfma", "kernel": "fp8_prep + fp8_gemm_kernel (4 products per step, timed together)",
+        return {"bound": "mfma", "kernel": f"fp8_prep + fp8_gemm_kernel, {_fp8_terms()} e4m3 term(s) (4 products per "
+                                           "step, timed together)",
                 "achieved": round(achieved, 2), "peak": PEAK_FP8_TFLOPS, "unit": "TFLOP/s",
                 "frac": round(achieved / PEAK_FP8_TFLOPS, 4), "traffic": None}
     kernel = ("grouped_gemm_kernel (register-staged, NF4 decoded in registers; 4 launches per step)"
@@ -167,6 +169,10 @@ def roofline(c, achieved, config):
     return {"bound": "mfma", "kernel": kernel, "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
             "traffic": read_traffic() if config == 1 else None}
+
+
+def _fp8_terms():
+    return 1 if os.environ.get("MEEPSQUARED_FP8_TERMS") == "1" else 2
 
 
 def copy_calibration(mib: int, reps: int = 3):
@@ -196,9 +202,10 @@ def main():
                     help="1: the bf16 Qwen3-shaped layer (default, the headline); 2: Mixtral-shaped with Zipf-loaded "
                          "experts; 3: config 1 with fp8 e4m3 stacks (per-row scales) on the fp8 MFMA; 4: config 1 "
                          "shapes on a packed varlen batch with NF4 stacks")
-    ap.add_argument("--bf16-products", action="store_true",
-                    help="config 3 with the products in bf16 (the fp8 stack decoded in registers, the reference's "
-                         "default for fp8 stacks) instead of on the fp8 MFMA")
+    ap.add_argument("--fp8-products", action="store_true",
+                    help="config 3 with the products on the fp8 MFMA, the activations quantised to two e4m3 terms "
+                         "(MEEPSQUARED_FP8_TERMS=1: one term, the reference's single pass, ~4.7 %% error) instead of "
+                         "in bf16 with the fp8 stack decoded in registers (the default: exact decode, faster here)")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {a.gpus})", file=sys.stderr)
@@ -224,9 +231,9 @@ def main():
         down8, down_s = _fp8.quantize_stack(down, per_row=True)
         del gate_up, down
         experts = Experts(gate_up8, down8, gate_up_proj_scale_inv=gate_up_s, down_proj_scale_inv=down_s)
-        os.environ["MEEPSQUARED_FP8_PRODUCTS"] = "0" if a.bf16_products else "1"
-        if a.bf16_products:
-            c = dict(c, name=c["name"] + ", bf16 products (fp8 stacks decoded in registers)")
+        os.environ["MEEPSQUARED_FP8_PRODUCTS"] = "1" if a.fp8_products else "0"
+        c = dict(c, name=c["name"] + (f", products on the fp8 MFMA ({_fp8_terms()} e4m3 activation term(s))"
+                                      if a.fp8_products else ", bf16 products (fp8 stacks decoded in registers)"))
     elif c.get("stack") == "nf4":
         from meepsquared_amd import _nf4
 
@@ -309,8 +316,8 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": {"fp8": "bf16 products (fp8-e4m3 stacks decoded in registers, per-row fp32 scales)" if a.bf16_products
-                  else "fp8-e4m3 products (bf16 activations, per-row fp32 stack scales)",
+        "dtype": {"fp8": "fp8-e4m3 products (activations as e4m3 terms, per-row fp32 stack scales)" if a.fp8_products
+                  else "bf16 products (fp8-e4m3 stacks decoded in registers, per-row fp32 scales)",
                   "nf4": "bf16 products (NF4 stacks decoded in registers)"}.get(c.get("stack"), "bf16"),
         "data": "synthetic (seeded N(0,1) x and logits, N(0,0.02) W, Kaiming-uniform A, N(0,0.01) B)",
         "config": {"workload": c["name"], "tokens": T, "hidden": H, "moe_intermediate": I, "experts": E,

@@ -237,24 +237,30 @@ int mlora_transpose_u8(const void* src, int64_t E, int64_t A, int64_t B, int64_t
  * ------------------------------------------------------------------------------------------- */
 
 /* Activations for the fp8 products, one pass over x (rows, K) bf16: for every row and every 64
- * columns a power-of-two scale 2^e with amax·2^-e <= 448, stored as E8M0 (127 + e) in
- * xs[block * ldxs + row] (int32), and x8[row * ld8 + k] = e4m3(x·2^-e) rounded to nearest even
- * (ld8 >= K rounded up to 64; the columns past K of the last block are zero).  colscale (NULL or
- * per expert colscale[e * cs_se + k]) multiplies the values before quantisation (a per-row stack
- * scale along k).  With at != NULL (A_e^T, as mlora_grouped_gemm's) low = bf16(x · A_e) from the
- * bf16 values, fp32 accumulation.  K % 16 == 0.  Replaces the X_FP8 quantisation inside
- * src/meepsquared/_grouped.py:191-194 (per row and BLOCK_K tile, scale amax/448), with the tile 64
- * and the scale rounded up to a power of two. */
-int mlora_fp8_prep(const void* x, int64_t ldx, int64_t rows, int K, const float* colscale, int64_t cs_se,
+ * columns a power-of-two scale 2^e with amax·2^-e <= 448, stored as E8M0 (127 + e) in byte 0 of
+ * xs[block * ldxs + row] (int32), and the 64 values e4m3(x·2^-e) rounded to nearest even.  terms = 1:
+ * x8[row * ld8 + k] (ld8 >= K rounded up to 64; the columns past K of the last block are zero).
+ * terms = 2: also the residual r = x - e4m3 value·2^e (exact in fp32) quantised the same way with its
+ * own scale 2^e2 (byte 1 of the xs word): row r's bytes of block b are the first term's 64 at
+ * x8[row * ld8 + 128b ..] and the residual's 64 after them (ld8 >= 2 · K rounded up to 64); x is
+ * then represented to within 2^-7 of each block's amax instead of 2^-4.  colscale (NULL or per
+ * expert colscale[e * cs_se + k]) multiplies the values before quantisation (a per-row stack scale
+ * along k).  With at != NULL (A_e^T, as mlora_grouped_gemm's) low = bf16(x · A_e) from the bf16
+ * values, fp32 accumulation.  K % 16 == 0.  Replaces the X_FP8 quantisation inside
+ * src/meepsquared/_grouped.py:191-194 (per row and BLOCK_K tile, scale amax/448, one term), with the
+ * tile 64 and the scale rounded up to a power of two. */
+int mlora_fp8_prep(const void* x, int64_t ldx, int64_t rows, int K, int terms, const float* colscale, int64_t cs_se,
                    void* x8, int64_t ld8, int32_t* xs, int64_t ldxs, const void* at, int64_t at_se, int64_t at_sr,
                    int rank, void* low, int64_t ldl, const int32_t* offsets, int E, void* stream);
 
-/* out[row, n] = c · sum_k x8·2^(xs-127) W8_e[n][k] + scaling · low[row,:] · B_e[:, n] + bias[e, n] on
- * v_mfma_scale_f32_32x32x64_f8f6f4: x8/xs from mlora_fp8_prep; w the fp8 e4m3 stack with k
- * contiguous, W8_e[n][k] = w[e*w_se + n*w_sn + k] (bytes); c = 1, scale[e] or scale[e*scale_se + n];
- * low (rows, rank) bf16 and bt = B_e^T as in mlora_grouped_gemm, or low = NULL.  Rows past
- * offsets[E-1] untouched.  Replaces _grouped_gemm_kernel with X_FP8 (src/meepsquared/_grouped.py:120-221). */
-int mlora_fp8_gemm(const void* x8, int64_t ld8, const int32_t* xs, int64_t ldxs, int64_t rows, int K, int N,
+/* out[row, n] = c · sum_k x̃[row, k] W8_e[n][k] + scaling · low[row,:] · B_e[:, n] + bias[e, n] on
+ * v_mfma_scale_f32_32x32x64_f8f6f4, x̃ the activations of mlora_fp8_prep with the same terms (two
+ * terms: one MFMA per term, each with its own scale byte); w the fp8 e4m3 stack with k contiguous,
+ * W8_e[n][k] = w[e*w_se + n*w_sn + k] (bytes); c = 1, scale[e] or scale[e*scale_se + n]; low
+ * (rows, rank) bf16 and bt = B_e^T as in mlora_grouped_gemm, or low = NULL.  Rows past offsets[E-1]
+ * untouched.  E <= 4096 (one term) or 3328 (two).  Replaces _grouped_gemm_kernel with X_FP8
+ * (src/meepsquared/_grouped.py:120-221). */
+int mlora_fp8_gemm(const void* x8, int64_t ld8, const int32_t* xs, int64_t ldxs, int64_t rows, int K, int terms, int N,
                    const void* w, int64_t w_se, int64_t w_sn, const float* scale, int scale_kind, int64_t scale_se,
                    const void* low, int64_t ldli, const void* bt, int64_t bt_se, int64_t bt_sn, int rank,
                    float scaling, const void* bias, int64_t bias_se, void* out, int64_t ldo,

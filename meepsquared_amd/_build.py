@@ -51,6 +51,12 @@ def build(jobs: int | None = None) -> Path:
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"linking libmlora.so failed:\n{proc.stderr}")
+    # a symbol of this library left undefined (a kernel stub the host pass did not emit) would only
+    # show when the library is loaded: refuse it here
+    nm = subprocess.run(["nm", "-D", "--undefined-only", str(tmp)], capture_output=True, text=True)
+    missing = [line.split()[-1] for line in nm.stdout.splitlines() if "mlora" in line]
+    if nm.returncode == 0 and missing:
+        raise RuntimeError(f"libmlora.so leaves its own symbols undefined: {missing[:5]}")
     os.replace(tmp, LIBRARY)
     return LIBRARY
 

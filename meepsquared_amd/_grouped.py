@@ -259,6 +259,13 @@ def fp8_products(device=None) -> bool:
     return os.environ.get("MEEPSQUARED_FP8_PRODUCTS") == "1"
 
 
+def fp8_product_terms() -> int:
+    """The e4m3 terms the fp8 products quantise the activations into: 2 (x ≈ hi + lo, within 2^-7 of each
+    64-column block's amax: the layer stays within 3e-2 of float32), or 1 with MEEPSQUARED_FP8_TERMS=1 (the
+    reference's single pass, src/meepsquared/_grouped.py:191-194: ~4-5 % error at config 1)."""
+    return 1 if os.environ.get("MEEPSQUARED_FP8_TERMS") == "1" else 2
+
+
 def _x_fp8(weight, products_fp8) -> bool:
     """The reference's X_FP8 (src/meepsquared/_grouped.py:320): only an fp8 stack, and then the switch."""
     w_fp8 = isinstance(weight, torch.Tensor) and weight.dtype == torch.float8_e4m3fn
@@ -284,8 +291,9 @@ def _k_contiguous(weight, w_se, w_sk, w_sn, K, N):
 
 
 def _launch_fp8(x, weight, scale, offsets, is_transposed, adapters, scaling, bias, store_low, backward):
-    """The fp8 products: one fp8_prep pass over x (e4m3 values, power-of-two scales per row and 64
-    columns, and low = bf16(x · A_e)), then the fp8 grouped product on the block-scaled MFMA."""
+    """The fp8 products: one fp8_prep pass over x (e4m3 terms, power-of-two scales per row and 64
+    columns, and low = bf16(x · A_e)), then the fp8 grouped product on the block-scaled MFMA, one MFMA
+    per term."""
     rows, K = x.shape
     if K % 16:
         raise ValueError(f"the fp8 products need in={K} to be a multiple of 16")
@@ -306,7 +314,8 @@ def _launch_fp8(x, weight, scale, offsets, is_transposed, adapters, scaling, bia
         colscale, cs_se, scale, scale_kind, scale_se = scale, scale_se, None, _lib.SCALE_NONE, 0
     w8, w_se, w_sn = _k_contiguous(weight, w_se, w_sk, w_sn, K, N)
     nkb = (K + 63) // 64
-    x8 = torch.empty((rows, nkb * 64), device=x.device, dtype=torch.uint8)
+    terms = fp8_product_terms()
+    x8 = torch.empty((rows, terms * nkb * 64), device=x.device, dtype=torch.uint8)
     xs = torch.empty((nkb, rows), device=x.device, dtype=torch.int32)
     E = offsets.numel()
     if bias is not None:
@@ -315,14 +324,15 @@ def _launch_fp8(x, weight, scale, offsets, is_transposed, adapters, scaling, bia
             bias = bias.contiguous()
     at = adapters.at if adapters is not None else None
     bt = adapters.bt if adapters is not None else None
-    info = {"rows": rows, "K": K, "N": N, "rank": adapters.rank if adapters is not None else 0, "fp8": True}
+    info = {"rows": rows, "K": K, "N": N, "rank": adapters.rank if adapters is not None else 0, "fp8": True,
+            "terms": terms}
     if launch_observer is not None:
         launch_observer("grouped_gemm", "before", info)
     stream = _lib.stream(x.device)
-    call("mlora_fp8_prep", ptr(x), x.stride(0), rows, K, ptr(colscale), cs_se, ptr(x8), x8.stride(0), ptr(xs),
+    call("mlora_fp8_prep", ptr(x), x.stride(0), rows, K, terms, ptr(colscale), cs_se, ptr(x8), x8.stride(0), ptr(xs),
          xs.stride(0), ptr(at), at.stride(0) if at is not None else 0, at.stride(1) if at is not None else 0, R,
          ptr(low), low.stride(0) if low is not None else 0, ptr(offsets), E, stream)
-    call("mlora_fp8_gemm", ptr(x8), x8.stride(0), ptr(xs), xs.stride(0), rows, K, N, ptr(w8), w_se, w_sn,
+    call("mlora_fp8_gemm", ptr(x8), x8.stride(0), ptr(xs), xs.stride(0), rows, K, terms, N, ptr(w8), w_se, w_sn,
          ptr(scale), scale_kind, scale_se, ptr(low), low.stride(0) if low is not None else 0,
          ptr(bt), bt.stride(0) if bt is not None else 0, bt.stride(1) if bt is not None else 0, R, float(scaling),
          ptr(bias), bias.stride(0) if bias is not None else 0, ptr(out), out.stride(0), ptr(offsets), E, stream)

@@ -52,8 +52,9 @@ SIGNATURES = {
     "mlora_combine_backward": (c_int, [P, P, I64, P, c_int, P, I64, c_int, P, c_int, P, P, P]),
     "mlora_transpose": (c_int, [P, I64, I64, I64, I64, I64, I64, P, P]),
     "mlora_transpose_u8": (c_int, [P, I64, I64, I64, I64, I64, I64, P, P]),
-    "mlora_fp8_prep": (c_int, [P, I64, I64, c_int, P, I64, P, I64, P, I64, P, I64, I64, c_int, P, I64, P, c_int, P]),
-    "mlora_fp8_gemm": (c_int, [P, I64, P, I64, I64, c_int, c_int, P, I64, I64, P, c_int, I64, P, I64, P, I64, I64,
+    "mlora_fp8_prep": (c_int, [P, I64, I64, c_int, c_int, P, I64, P, I64, P, I64, P, I64, I64, c_int, P, I64, P, c_int,
+                               P]),
+    "mlora_fp8_gemm": (c_int, [P, I64, P, I64, I64, c_int, c_int, c_int, P, I64, I64, P, c_int, I64, P, I64, P, I64, I64,
                                c_int, c_float, P, I64, P, I64, P, c_int, P]),
     "mlora_fp8_quantize": (c_int, [P, c_int, I64, I64, I64, c_int, c_int, P, P, P]),
     "mlora_fp8_dequantize": (c_int, [P, P, I64, I64, I64, c_int, c_int, P, c_int, P]),

@@ -45,8 +45,8 @@ struct PrepArgs {
   const float* colscale;  // NULL, or per-column multipliers of the quantised values: colscale[e*cs_se + k]
   int64_t cs_se;
   uint8_t* x8;
-  int64_t ld8;            // >= K rounded up to 64; columns K .. ld8-1 of the 64-block are written as zero
-  int32_t* xs;            // E8M0 scale of row r, block b at xs[b * ldxs + r]
+  int64_t ld8;            // >= TERMS * (K rounded up to 64); the 64-block's columns past K are written as zero
+  int32_t* xs;            // E8M0 scale of row r, block b at xs[b * ldxs + r] (two terms: byte 1 the lo term's)
   int64_t ldxs;
   const bf16* at;         // A_e^T (E, R, K) k contiguous, or NULL
   int64_t at_se, at_sr;
@@ -111,7 +111,9 @@ __device__ __forceinline__ uint32_t e8m0_for(float amax) {
   return (uint32_t)(byte < 0 ? 0 : (byte > 254 ? 254 : byte));
 }
 
-template <int NRB>
+// TERMS = 2: each 64-column block also gets the residual x - hi·2^e1 (exact in fp32) quantised the same
+// way with its own scale 2^e2; row r's bytes of block b are hi at 128b .. 128b+63, lo at 128b+64 ..
+template <int NRB, int TERMS>
 __global__ __launch_bounds__(PT) void fp8_prep_kernel(PrepArgs p) {
   constexpr int R = NRB * 16;
   __shared__ __attribute__((aligned(16))) bf16 xt[PR * XP];               // the 64 x 64 chunk of x
@@ -168,9 +170,32 @@ __global__ __launch_bounds__(PT) void fp8_prep_kernel(PrepArgs p) {
       u32x2 q = {0u, 0u};
 #pragma unroll
       for (int j = 0; j < 8; ++j) q[j >> 2] |= f32_to_e4m3(f[j] * inv) << (8 * (j & 3));
+      uint32_t word = eb;
+      u32x2 q2 = {0u, 0u};
+      if constexpr (TERMS == 2) {
+        // the residual of each value after its hi term (exact: the hi term is within a factor two of
+        // the value, or zero), then its block's scale and bytes
+        const float sc = __uint_as_float(eb << 23);  // 2^(eb - 127)
+        float amax2 = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          f[j] -= fp8_e4m3_to_f32((q[j >> 2] >> (8 * (j & 3))) & 0xFFu) * sc;
+          amax2 = fmaxf(amax2, fabsf(f[j]));
+        }
+        amax2 = fmaxf(amax2, __shfl_xor(amax2, 1, 64));
+        amax2 = fmaxf(amax2, __shfl_xor(amax2, 2, 64));
+        amax2 = fmaxf(amax2, __shfl_xor(amax2, 4, 64));
+        const uint32_t eb2 = e8m0_for(amax2);
+        const float inv2 = __uint_as_float((254u - eb2) << 23);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) q2[j >> 2] |= f32_to_e4m3(f[j] * inv2) << (8 * (j & 3));
+        word |= eb2 << 8;
+      }
       if (row < mrows) {
-        *(u32x2*)(p.x8 + (row0 + row) * p.ld8 + col) = q;
-        if (cc == 0) p.xs[(int64_t)kb * p.ldxs + row0 + row] = (int32_t)eb;
+        uint8_t* dst = p.x8 + (row0 + row) * p.ld8 + (int64_t)kb * PR * TERMS + cc * 8;
+        *(u32x2*)dst = q;
+        if constexpr (TERMS == 2) *(u32x2*)(dst + PR) = q2;
+        if (cc == 0) p.xs[(int64_t)kb * p.ldxs + row0 + row] = (int32_t)word;
       }
       if constexpr (NRB > 0) *(u32x4*)(xt + row * XP + cc * 8) = v;
     }
@@ -213,20 +238,31 @@ __global__ __launch_bounds__(PT) void fp8_prep_kernel(PrepArgs p) {
 // ------------------------------------------------------------------------------------------------
 // the fp8 grouped product
 // ------------------------------------------------------------------------------------------------
-constexpr int BM = 256, BN = 256, BK = 64, STAGES = 4;  // BK in fp8 elements (bytes)
+constexpr int BM = 256, BN = 256, BK = 64;  // BK in fp8 elements (bytes) per term
 constexpr int WAVES_M = 2, WAVES_N = 4, NW = 8, kThreads = 512;
 constexpr int FM = BM / WAVES_M / 32, FN = BN / WAVES_N / 32;
-constexpr int XI = BM * BK / 16 / (64 * NW), WI = BN * BK / 16 / (64 * NW);  // 16-byte DMA copies per wave
-constexpr int PS = XI + WI + 1;  // and one 4-byte copy of 64 rows' scale words
-constexpr int SLOT_RING = BM * BK + BN * BK + BM * 4;  // bytes: x8, W8, scale words
+constexpr int WI = BN * BK / 16 / (64 * NW);  // 16-byte DMA copies of the stack tile per wave
+// TERMS activation terms (1: e4m3 values; 2: hi and lo): a stage holds 64 k of each, the x rows
+// 64 * TERMS bytes long; four ring slots for one term, three for two (LDS)
+template <int TERMS>
+struct Cfg {
+  static constexpr int XB = BK * TERMS;                 // bytes of one x row per stage
+  static constexpr int CH = XB / 16;                    // its 16-byte chunks
+  static constexpr int XI = BM * XB / 16 / (64 * NW);   // x copies per wave per stage
+  static constexpr int PS = XI + WI + 1;                // and one 4-byte copy of 64 rows' scale words
+  static constexpr int STAGES = TERMS == 2 ? 3 : 4;
+  static constexpr int RING = BM * XB + BN * BK + BM * 4;  // bytes of a slot: x, W8, scale words
+};
 // a slot also holds one of the epilogue's [256][RP + 8] bf16 tiles
-template <int NRB>
+template <int NRB, int TERMS>
 struct Slot {
   static constexpr int kEpi = BM * (NRB * 16 + 8) * 2;
-  static constexpr int kBytes = SLOT_RING > kEpi ? SLOT_RING : kEpi;
+  static constexpr int kBytes = Cfg<TERMS>::RING > kEpi ? Cfg<TERMS>::RING : kEpi;
 };
-static_assert(4 * Slot<4>::kBytes + 4096 * 4 <= 163840, "four slots and the largest tile map fit in LDS");
-static_assert(XI == 2 && WI == 2, "tile split");
+static_assert(4 * Slot<4, 1>::kBytes + 4096 * 4 <= 163840, "four one-term slots and the largest tile map fit in LDS");
+constexpr int kMaxE2 = (163840 - 3 * Slot<4, 2>::kBytes) / 4;  // experts whose tile map fits beside three two-term slots
+static_assert(kMaxE2 >= 1024, "three two-term slots leave room for the tile map");
+static_assert(Cfg<1>::XI == 2 && Cfg<2>::XI == 4 && WI == 2, "tile split");
 
 struct Args {
   GemmArgs g;          // x unused; w = the fp8 stack with k contiguous (w_sk == 1); low unused
@@ -240,6 +276,15 @@ struct Args {
 
 // rows of 64 bytes, 16-byte chunk c of row r in slot c ^ ((r >> 2) & 3)
 __device__ __forceinline__ int swz(int row, int chunk) { return row * BK + ((chunk ^ ((row >> 2) & 3)) << 4); }
+// x rows of 64 * TERMS bytes: four chunks as above; eight: chunk c of row r in slot c ^ ((r >> 1) & 7),
+// so the eight rows eight consecutive lanes read (two per 256-byte bank span) hit eight bank groups
+template <int TERMS>
+__device__ __forceinline__ int swzx(int row, int chunk) {
+  if constexpr (TERMS == 1) return swz(row, chunk);
+  else return row * Cfg<TERMS>::XB + ((chunk ^ ((row >> 1) & 7)) << 4);
+}
+template <int TERMS>
+__device__ __forceinline__ int swzx_f(int row) { return TERMS == 1 ? (row >> 2) & 3 : (row >> 1) & 7; }
 
 template <int N>
 __device__ __forceinline__ void wait_vm() {
@@ -253,7 +298,9 @@ __device__ __forceinline__ void stage_barrier() {
   asm volatile("" ::: "memory");
 }
 
+template <int TERMS>
 struct Feed {
+  static constexpr int XI = Cfg<TERMS>::XI, CH = Cfg<TERMS>::CH, XB = Cfg<TERMS>::XB;
   rsrc_t rx, rw, rs;
   uint32_t xo[XI], wo[WI], so;
   int xk[XI], wk[WI];
@@ -270,9 +317,9 @@ struct Feed {
 #pragma unroll
     for (int q = 0; q < XI; ++q) {
       const int instr = wave * XI + q, ci = instr * 64 + lane;
-      const int row = ci >> 2, c = (ci & 3) ^ ((row >> 2) & 3);
+      const int row = ci / CH, c = (ci % CH) ^ swzx_f<TERMS>(row);
       xo[q] = (uint32_t)(row * a.ld8 + c * 16);
-      xk[q] = c * 16;
+      xk[q] = (c % 4) * 16;  // the chunk's first k within its term
       xd[q] = instr * 1024;
     }
 #pragma unroll
@@ -282,11 +329,11 @@ struct Feed {
       const int n = n0 + row;
       wo[q] = n < p.N ? (uint32_t)((int64_t)n * p.w_sn + c * 16) : 0u;
       wk[q] = n < p.N ? c * 16 : (1 << 30);
-      wd[q] = BM * BK + instr * 1024;
+      wd[q] = BM * XB + instr * 1024;
     }
     // wave w copies the scale words of rows 64 (w % 4) .. +63 (waves w and w + 4 the same ones)
     so = (uint32_t)((64 * (wave & 3) + lane) * 4);
-    sd = BM * BK + BN * BK + 256 * (wave & 3);
+    sd = BM * XB + BN * BK + 256 * (wave & 3);
   }
 
   __device__ __forceinline__ void issue(const Args& a, uint8_t* slot, int kt) const {
@@ -294,7 +341,7 @@ struct Feed {
 #pragma unroll
     for (int q = 0; q < XI; ++q)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_void*)(slot + xd[q]), 16,
-                                               xk[q] + k0 < ld8 ? xo[q] + (uint32_t)k0 : kOob, 0, 0, 0);
+                                               xk[q] + k0 < K ? xo[q] + (uint32_t)(k0 * TERMS) : kOob, 0, 0, 0);
 #pragma unroll
     for (int q = 0; q < WI; ++q)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_void*)(slot + wd[q]), 16,
@@ -304,20 +351,29 @@ struct Feed {
   }
 };
 
-template <int AM>
+// 32 fp8 values of MFMA operand row r: this lane's half (32 k) of term t's 64, from a row of 64*TERMS bytes
+template <int TERMS>
+__device__ __forceinline__ v8i x_frag(const uint8_t* xs8, int r, int term, int lane) {
+  const int c0 = 4 * term + 2 * (lane >> 5);
+  const u32x4 lo = *(const u32x4*)(xs8 + swzx<TERMS>(r, c0));
+  const u32x4 hi = *(const u32x4*)(xs8 + swzx<TERMS>(r, c0 + 1));
+  return v8i{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+}
+
+template <int AM, int TERMS>
 __device__ __forceinline__ void compute(const uint8_t* slot, int lane, int wm, int wn, f32x16 (&acc)[FM][FN]) {
   if constexpr (AM > 0) {
+    constexpr int XB = Cfg<TERMS>::XB;
     const uint8_t* xs8 = slot;
-    const uint8_t* ws8 = slot + BM * BK;
-    const int32_t* sw = (const int32_t*)(slot + BM * BK + BN * BK);
-    v8i xf[AM], wf[FN];
+    const uint8_t* ws8 = slot + BM * XB;
+    const int32_t* sw = (const int32_t*)(slot + BM * XB + BN * BK);
+    v8i xf[AM][TERMS], wf[FN];
     int sx[AM];
 #pragma unroll
     for (int i = 0; i < AM; ++i) {
       const int r = (i * WAVES_M + wm) * 32 + (lane & 31);
-      const u32x4 lo = *(const u32x4*)(xs8 + swz(r, 2 * (lane >> 5)));
-      const u32x4 hi = *(const u32x4*)(xs8 + swz(r, 2 * (lane >> 5) + 1));
-      xf[i] = v8i{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+#pragma unroll
+      for (int t = 0; t < TERMS; ++t) xf[i][t] = x_frag<TERMS>(xs8, r, t, lane);
       sx[i] = sw[r];
     }
 #pragma unroll
@@ -327,37 +383,54 @@ __device__ __forceinline__ void compute(const uint8_t* slot, int lane, int wm, i
       const u32x4 hi = *(const u32x4*)(ws8 + swz(n, 2 * (lane >> 5) + 1));
       wf[j] = v8i{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
     }
+    // term t's scale is byte t of the row's scale word (the MFMA's scale operand selects the byte)
 #pragma unroll
     for (int i = 0; i < AM; ++i)
 #pragma unroll
-      for (int j = 0; j < FN; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wf[j], xf[i], acc[i][j], 0, 0, 0, 127, 0, sx[i]);
+      for (int j = 0; j < FN; ++j) {
+        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wf[j], xf[i][0], acc[i][j], 0, 0, 0, 127, 0, sx[i]);
+        if constexpr (TERMS == 2)
+          acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wf[j], xf[i][1], acc[i][j], 0, 0, 0, 127, 1, sx[i]);
+      }
   }
 }
 
-template <int S, int AM>
-__device__ __forceinline__ void stage(const Args& a, const Feed& f, uint8_t* const (&slots)[STAGES], int kt, int lane,
-                                      int wm, int wn, f32x16 (&acc)[FM][FN]) {
-  wait_vm<PS * (STAGES - 2)>();
+template <int S, int AM, int TERMS>
+__device__ __forceinline__ void stage(const Args& a, const Feed<TERMS>& f, uint8_t* const (&slots)[4],
+                                      int kt, int lane, int wm, int wn, f32x16 (&acc)[FM][FN]) {
+  constexpr int ST = Cfg<TERMS>::STAGES;
+  wait_vm<Cfg<TERMS>::PS * (ST - 2)>();
   stage_barrier();
-  f.issue(a, slots[(S + STAGES - 1) % STAGES], kt + STAGES - 1);
-  compute<AM>(slots[S], lane, wm, wn, acc);
+  f.issue(a, slots[(S + ST - 1) % ST], kt + ST - 1);
+  compute<AM, TERMS>(slots[S], lane, wm, wn, acc);
 }
 
-template <int AM>
-__device__ __forceinline__ void kloop(const Args& a, const Feed& f, uint8_t* const (&slots)[STAGES], int nk, int lane,
-                                      int wm, int wn, f32x16 (&acc)[FM][FN]) {
+template <int AM, int TERMS>
+__device__ __forceinline__ void kloop(const Args& a, const Feed<TERMS>& f, uint8_t* const (&slots)[4],
+                                      int nk, int lane, int wm, int wn, f32x16 (&acc)[FM][FN]) {
+  constexpr int ST = Cfg<TERMS>::STAGES;
   int kt = 0;
-  for (; kt + STAGES <= nk; kt += STAGES) {
-    stage<0, AM>(a, f, slots, kt, lane, wm, wn, acc);
-    stage<1, AM>(a, f, slots, kt + 1, lane, wm, wn, acc);
-    stage<2, AM>(a, f, slots, kt + 2, lane, wm, wn, acc);
-    stage<3, AM>(a, f, slots, kt + 3, lane, wm, wn, acc);
+  if constexpr (ST == 4) {
+    for (; kt + 4 <= nk; kt += 4) {
+      stage<0, AM, TERMS>(a, f, slots, kt, lane, wm, wn, acc);
+      stage<1, AM, TERMS>(a, f, slots, kt + 1, lane, wm, wn, acc);
+      stage<2, AM, TERMS>(a, f, slots, kt + 2, lane, wm, wn, acc);
+      stage<3, AM, TERMS>(a, f, slots, kt + 3, lane, wm, wn, acc);
+    }
+    const int rem = nk - kt;
+    if (rem > 0) stage<0, AM, TERMS>(a, f, slots, kt, lane, wm, wn, acc);
+    if (rem > 1) stage<1, AM, TERMS>(a, f, slots, kt + 1, lane, wm, wn, acc);
+    if (rem > 2) stage<2, AM, TERMS>(a, f, slots, kt + 2, lane, wm, wn, acc);
+  } else {
+    for (; kt + 3 <= nk; kt += 3) {
+      stage<0, AM, TERMS>(a, f, slots, kt, lane, wm, wn, acc);
+      stage<1, AM, TERMS>(a, f, slots, kt + 1, lane, wm, wn, acc);
+      stage<2, AM, TERMS>(a, f, slots, kt + 2, lane, wm, wn, acc);
+    }
+    const int rem = nk - kt;
+    if (rem > 0) stage<0, AM, TERMS>(a, f, slots, kt, lane, wm, wn, acc);
+    if (rem > 1) stage<1, AM, TERMS>(a, f, slots, kt + 1, lane, wm, wn, acc);
   }
-  const int rem = nk - kt;
-  if (rem > 0) stage<0, AM>(a, f, slots, kt, lane, wm, wn, acc);
-  if (rem > 1) stage<1, AM>(a, f, slots, kt + 1, lane, wm, wn, acc);
-  if (rem > 2) stage<2, AM>(a, f, slots, kt + 2, lane, wm, wn, acc);
 }
 
 // the tile map of BM-row tiles (as the bf16 kernel's)
@@ -375,18 +448,19 @@ __device__ __forceinline__ Item decode(const GemmArgs& p, int64_t item, int nb, 
   return it;
 }
 
-template <int NRB>
+template <int NRB, int TERMS>
 __global__ __launch_bounds__(kThreads, 1) void fp8_gemm_kernel(Args a) {
   constexpr int RP = NRB * 16;
   constexpr int LP = RP + 8;
-  constexpr int SB = Slot<NRB>::kBytes;
+  constexpr int SB = Slot<NRB, TERMS>::kBytes;
+  constexpr int ST = Cfg<TERMS>::STAGES;
   __shared__ __attribute__((aligned(16))) uint8_t slot0[SB];
   __shared__ __attribute__((aligned(16))) uint8_t slot1[SB];
   __shared__ __attribute__((aligned(16))) uint8_t slot2[SB];
-  __shared__ __attribute__((aligned(16))) uint8_t slot3[SB];
+  __shared__ __attribute__((aligned(16))) uint8_t slot3[ST == 4 ? SB : 16];
   extern __shared__ __attribute__((aligned(16))) int tend[];
   static_assert(BM * LP * 2 <= SB && BN * LP * 2 <= SB, "the epilogue's tiles fit in a slot");
-  uint8_t* const slots[STAGES] = {slot0, slot1, slot2, slot3};
+  uint8_t* const slots[4] = {slot0, slot1, slot2, ST == 4 ? slot3 : slot0};  // three slots: the fourth unused
   const GemmArgs& p = a.g;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -408,7 +482,7 @@ __global__ __launch_bounds__(kThreads, 1) void fp8_gemm_kernel(Args a) {
     const int64_t row0 = it.row0;
     const int mb = (mrows + 31) >> 5;
     const int am = min(FM, max(0, (mb - wm + WAVES_M - 1) / WAVES_M));
-    Feed f;
+    Feed<TERMS> f;
     f.init(a, row0, mrows, e, n0, wave, lane);
     f32x16 acc[FM][FN];
 #pragma unroll
@@ -418,13 +492,13 @@ __global__ __launch_bounds__(kThreads, 1) void fp8_gemm_kernel(Args a) {
 
     __syncthreads();  // the previous item's epilogue is done with the LDS
 #pragma unroll
-    for (int s = 0; s < STAGES - 1; ++s) f.issue(a, slots[s], s);
+    for (int s = 0; s < ST - 1; ++s) f.issue(a, slots[s], s);
     switch (am) {
-      case 4: kloop<4>(a, f, slots, nk, lane, wm, wn, acc); break;
-      case 3: kloop<3>(a, f, slots, nk, lane, wm, wn, acc); break;
-      case 2: kloop<2>(a, f, slots, nk, lane, wm, wn, acc); break;
-      case 1: kloop<1>(a, f, slots, nk, lane, wm, wn, acc); break;
-      default: kloop<0>(a, f, slots, nk, lane, wm, wn, acc); break;
+      case 4: kloop<4, TERMS>(a, f, slots, nk, lane, wm, wn, acc); break;
+      case 3: kloop<3, TERMS>(a, f, slots, nk, lane, wm, wn, acc); break;
+      case 2: kloop<2, TERMS>(a, f, slots, nk, lane, wm, wn, acc); break;
+      case 1: kloop<1, TERMS>(a, f, slots, nk, lane, wm, wn, acc); break;
+      default: kloop<0, TERMS>(a, f, slots, nk, lane, wm, wn, acc); break;
     }
     wait_vm<0>();
     __syncthreads();
@@ -503,9 +577,21 @@ __global__ __launch_bounds__(kThreads, 1) void fp8_gemm_kernel(Args a) {
   }
 }
 
-template <int NRB>
+// every variant instantiated here: clang otherwise left some host stubs undefined (the library then fails to load)
+template __global__ void fp8_gemm_kernel<0, 1>(Args);
+template __global__ void fp8_gemm_kernel<1, 1>(Args);
+template __global__ void fp8_gemm_kernel<2, 1>(Args);
+template __global__ void fp8_gemm_kernel<3, 1>(Args);
+template __global__ void fp8_gemm_kernel<4, 1>(Args);
+template __global__ void fp8_gemm_kernel<0, 2>(Args);
+template __global__ void fp8_gemm_kernel<1, 2>(Args);
+template __global__ void fp8_gemm_kernel<2, 2>(Args);
+template __global__ void fp8_gemm_kernel<3, 2>(Args);
+template __global__ void fp8_gemm_kernel<4, 2>(Args);
+
+template <int NRB, int TERMS>
 static int launch_gemm(const Args& a, hipStream_t s) {
-  auto kern = fp8_gemm_kernel<NRB>;
+  auto kern = fp8_gemm_kernel<NRB, TERMS>;
   const size_t lds = (size_t)a.g.E * sizeof(int);
   static std::mutex mu;
   static std::unordered_map<int64_t, int> grid_cache;
@@ -542,7 +628,7 @@ using namespace mlora;
 
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
-extern "C" int mlora_fp8_prep(const void* x, int64_t ldx, int64_t rows, int K, const float* colscale, int64_t cs_se,
+extern "C" int mlora_fp8_prep(const void* x, int64_t ldx, int64_t rows, int K, int terms, const float* colscale, int64_t cs_se,
                               void* x8, int64_t ld8, int32_t* xs, int64_t ldxs, const void* at, int64_t at_se,
                               int64_t at_sr, int rank, void* low, int64_t ldl, const int32_t* offsets, int E,
                               void* stream) {
@@ -550,9 +636,11 @@ extern "C" int mlora_fp8_prep(const void* x, int64_t ldx, int64_t rows, int K, c
   if (rows < 0) return fail("fp8_prep: rows=%lld is negative", (long long)rows);
   if (E < 1 || E > 4096) return fail("fp8_prep: E=%d outside [1, 4096]", E);
   if (K < 16 || K % 16) return fail("fp8_prep: K=%d must be a positive multiple of 16", K);
+  if (terms != 1 && terms != 2) return fail("fp8_prep: terms=%d is neither 1 nor 2", terms);
   const int64_t kpad = (int64_t)(K + 63) / 64 * 64;
   if (ldx < K || ldx % 8 || !aligned16(x)) return fail("fp8_prep: x needs 16-byte aligned rows of >= K values");
-  if (ld8 < kpad || ld8 % 16 || !aligned16(x8)) return fail("fp8_prep: x8 needs 16-byte aligned rows of >= %lld bytes", (long long)kpad);
+  if (ld8 < terms * kpad || ld8 % 16 || !aligned16(x8))
+    return fail("fp8_prep: x8 needs 16-byte aligned rows of >= %lld bytes", (long long)(terms * kpad));
   if (ldxs < rows || ((uintptr_t)xs & 3u)) return fail("fp8_prep: xs needs a block stride >= rows");
   if (at != nullptr) {
     if (rank < 16 || rank > kMaxRank || rank % 16) return fail("fp8_prep: rank=%d must be 16, 32, 48 or 64", rank);
@@ -570,7 +658,11 @@ extern "C" int mlora_fp8_prep(const void* x, int64_t ldx, int64_t rows, int K, c
   const int grid = (int)(rows / f8::PR + E);
   const size_t lds = (size_t)E * sizeof(int);
   hipStream_t s = as_stream(stream);
-#define MLORA_PREP(NRB) hipLaunchKernelGGL(f8::fp8_prep_kernel<NRB>, dim3(grid), dim3(f8::PT), lds, s, p)
+#define MLORA_PREP(NRB)                                                                      \
+  do {                                                                                       \
+    if (terms == 2) hipLaunchKernelGGL((f8::fp8_prep_kernel<NRB, 2>), dim3(grid), dim3(f8::PT), lds, s, p); \
+    else hipLaunchKernelGGL((f8::fp8_prep_kernel<NRB, 1>), dim3(grid), dim3(f8::PT), lds, s, p);            \
+  } while (0)
   switch (at == nullptr ? 0 : rank / 16) {
     case 0: MLORA_PREP(0); break;
     case 1: MLORA_PREP(1); break;
@@ -582,7 +674,8 @@ extern "C" int mlora_fp8_prep(const void* x, int64_t ldx, int64_t rows, int K, c
   return launch_status("fp8_prep");
 }
 
-extern "C" int mlora_fp8_gemm(const void* x8, int64_t ld8, const int32_t* xs, int64_t ldxs, int64_t rows, int K, int N,
+extern "C" int mlora_fp8_gemm(const void* x8, int64_t ld8, const int32_t* xs, int64_t ldxs, int64_t rows, int K, int terms,
+                              int N,
                               const void* w, int64_t w_se, int64_t w_sn, const float* scale, int scale_kind,
                               int64_t scale_se, const void* low, int64_t ldli, const void* bt, int64_t bt_se,
                               int64_t bt_sn, int rank, float scaling, const void* bias, int64_t bias_se, void* out,
@@ -591,9 +684,12 @@ extern "C" int mlora_fp8_gemm(const void* x8, int64_t ld8, const int32_t* xs, in
   if (rows < 0) return fail("fp8_gemm: rows=%lld is negative", (long long)rows);
   if (E < 1 || E > 4096) return fail("fp8_gemm: E=%d outside [1, 4096]", E);
   if (K < 16 || K % 16) return fail("fp8_gemm: K=%d must be a positive multiple of 16", K);
+  if (terms != 1 && terms != 2) return fail("fp8_gemm: terms=%d is neither 1 nor 2", terms);
+  if (terms == 2 && E > f8::kMaxE2) return fail("fp8_gemm: E=%d past the %d experts of the two-term tile map", E, f8::kMaxE2);
   if (N < 8 || N % 8) return fail("fp8_gemm: N=%d must be a positive multiple of 8", N);
   const int64_t kpad = (int64_t)(K + 63) / 64 * 64;
-  if (ld8 < kpad || ld8 % 16 || !aligned16(x8)) return fail("fp8_gemm: x8 needs 16-byte aligned rows of >= %lld bytes", (long long)kpad);
+  if (ld8 < terms * kpad || ld8 % 16 || !aligned16(x8))
+    return fail("fp8_gemm: x8 needs 16-byte aligned rows of >= %lld bytes", (long long)(terms * kpad));
   if ((int64_t)f8::BM * ld8 > 0x7FFFFFF0) return fail("fp8_gemm: x8 row stride %lld too large", (long long)ld8);
   if (ldxs < rows || ((uintptr_t)xs & 3u)) return fail("fp8_gemm: xs needs a block stride >= rows");
   if (ldxs * (kpad / 64) * 4 > 0x7FFFFFF0) return fail("fp8_gemm: the scale words exceed 2 GiB");
@@ -626,11 +722,13 @@ extern "C" int mlora_fp8_gemm(const void* x8, int64_t ld8, const int32_t* xs, in
   a.x8 = (const uint8_t*)x8; a.ld8 = ld8; a.xs = xs; a.ldxs = ldxs;
   a.lowin = (const bf16*)low; a.ldli = ldli;
   hipStream_t s = as_stream(stream);
+#define MLORA_F8(NRB) return terms == 2 ? f8::launch_gemm<NRB, 2>(a, s) : f8::launch_gemm<NRB, 1>(a, s)
   switch (low == nullptr ? 0 : rank / 16) {
-    case 0: return f8::launch_gemm<0>(a, s);
-    case 1: return f8::launch_gemm<1>(a, s);
-    case 2: return f8::launch_gemm<2>(a, s);
-    case 3: return f8::launch_gemm<3>(a, s);
-    default: return f8::launch_gemm<4>(a, s);
+    case 0: MLORA_F8(0);
+    case 1: MLORA_F8(1);
+    case 2: MLORA_F8(2);
+    case 3: MLORA_F8(3);
+    default: MLORA_F8(4);
   }
+#undef MLORA_F8
 }

@@ -77,6 +77,43 @@ def fp8_rows_dequantize(q, e8m0, K):
     return v.view(rows, kp)[:, :K]
 
 
+def fp8_rows_quantize2(x, block=64, colscale=None):
+    """Two-term activations for the fp8 products: x ≈ hi·2^e1 + lo·2^e2 per row and `block` columns, hi
+    the one-term quantisation (fp8_rows_quantize) and lo the same rule applied to the residual
+    x - hi·2^e1, which is exact in fp32.  Returns (q uint8 (rows, 2 · K padded), per block b the hi bytes
+    at [2b·block, (2b+1)·block) and the lo bytes after them; words int32 (blocks, rows) = (127 + e1) |
+    (127 + e2) << 8).  No reference counterpart: the reference's fp8 products keep one term
+    (src/meepsquared/_grouped.py:191-194, 4.1 % error by design/grouped-lora-kernel.md:3).
+    Pinned by: hi is fp8_rows_quantize's result; lo is fp8_rows_quantize of the residual computed in
+    float64 (which equals the fp32 one); the reconstruction is within 2^-7 of each block's amax
+    (tests/test_oracle.py).
+    """
+    x = torch.as_tensor(x).float()
+    if colscale is not None:
+        x = x * torch.as_tensor(colscale).float()
+    rows, K = x.shape
+    hi, e1 = fp8_rows_quantize(x, block)
+    kp = hi.shape[1]
+    xp = torch.zeros(rows, kp)
+    xp[:, :K] = x
+    residual = xp - fp8_rows_dequantize(hi, e1, kp)
+    lo, e2 = fp8_rows_quantize(residual, block)
+    nb = kp // block
+    q = torch.stack([hi.view(rows, nb, block), lo.view(rows, nb, block)], dim=2).reshape(rows, 2 * kp)
+    return q, e1 | (e2 << 8)
+
+
+def fp8_rows_dequantize2(q, words, K):
+    """hi·2^e1 + lo·2^e2 per row and block (fp8_rows_quantize2's layout), the first K columns (float32)."""
+    rows, kp2 = q.shape
+    nb = words.shape[0]
+    block = kp2 // (2 * nb)
+    qq = q.view(rows, nb, 2, block)
+    hi = fp8_rows_dequantize(qq[:, :, 0].reshape(rows, nb * block).contiguous(), words & 0xFF, nb * block)
+    lo = fp8_rows_dequantize(qq[:, :, 1].reshape(rows, nb * block).contiguous(), (words >> 8) & 0xFF, nb * block)
+    return (hi + lo)[:, :K]
+
+
 def nf4_code_from_definition():
     """The 16 NF4 values from QLoRA's definition (Dettmers et al. 2023, Appendix E): 8 positive
     quantiles of N(0,1) from the upper half (offset 0.9677 = 1/2 (1/(2·15) + 1/(2·16)) mapped to

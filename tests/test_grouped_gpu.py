@@ -115,11 +115,8 @@ def test_the_product_with_adapters_and_its_gradients_match_pytorch(is_transposed
     tol = Q_TOL if fp8 else BF16_TOL
     for name, a, b in zip(("out", "grad_x", "grad_lhs", "grad_rhs"), got, expected):
         assert a.shape == b.shape, name
-        if products and name in ("out", "grad_x"):
-            # activations (and the output gradient) quantised to e4m3 per row and 64 columns: the
-            # reference's own bound for its fp8 products (tests/test_grouped.py:136-139)
-            assert rel(a, b) <= 0.06, (name, rel(a, b))
-            continue
+        # with fp8 products the activations (and the output gradient) are two e4m3 terms per row and 64
+        # columns: within BASELINE's 3e-2 like the stacks' own quantisation
         assert rel(a, b) < tol, (name, rel(a, b))
         # the reference's own bound (tests/test_grouped.py:141-143)
         torch.testing.assert_close(a.float(), b.float(), atol=1e-2 * b.float().abs().max().item(), rtol=0, msg=name)
@@ -303,10 +300,13 @@ def test_the_swapped_adapters_take_each_others_roles():
 
 
 @pytest.mark.parametrize("is_transposed", [False, True])
-def test_the_fp8_product_quantizes_the_activations_per_row_and_stays_close(is_transposed):
-    """Mirrors the reference's tests/test_grouped.py:68-81 (products_fp8=True)."""
+@pytest.mark.parametrize("terms", [1, 2])
+def test_the_fp8_product_quantizes_the_activations_per_row_and_stays_close(is_transposed, terms, monkeypatch):
+    """Mirrors the reference's tests/test_grouped.py:68-81 (products_fp8=True) with its bounds for one e4m3
+    term (the reference's single pass), and BASELINE's 3e-2 for the two terms this build uses by default."""
     from meepsquared_amd import grouped_linear
 
+    monkeypatch.setenv("MEEPSQUARED_FP8_TERMS", str(terms))
     torch.manual_seed(0)
     x = torch.randn(300, 128, device="cuda", dtype=torch.bfloat16)
     x[::7] *= 20  # rows of different sizes: the scale is per row
@@ -315,8 +315,12 @@ def test_the_fp8_product_quantizes_the_activations_per_row_and_stays_close(is_tr
     offsets = offsets_of([100, 0, 150, 50])
     expected = ref.reference(x, weight.float(), offsets.cpu(), is_transposed).float().cpu()
     out = grouped_linear(x, weight, offsets, is_transposed, products_fp8=True).float().cpu()
-    assert (out - expected).abs().max() <= 0.1 * expected.abs().max()
-    assert (out - expected).norm() / expected.norm() < 0.06
+    if terms == 1:
+        assert (out - expected).abs().max() <= 0.1 * expected.abs().max()
+        assert (out - expected).norm() / expected.norm() < 0.06
+    else:
+        assert (out - expected).abs().max() <= 0.01 * expected.abs().max()
+        assert (out - expected).norm() / expected.norm() < 3e-2
 
 
 def test_the_fp8_products_switch_follows_the_environment(monkeypatch):
@@ -330,9 +334,11 @@ def test_the_fp8_products_switch_follows_the_environment(monkeypatch):
     assert _grouped._x_fp8(w8, None) and not _grouped._x_fp8(w8, False)
 
 
+@pytest.mark.parametrize("terms", [1, 2])
 @pytest.mark.parametrize("K,colscale", [(208, False), (2048, False), (96, True)])
-def test_the_fp8_activation_pass_is_bit_exact(K, colscale):
-    """mlora_fp8_prep against the oracle: e4m3 bytes and E8M0 scales bit-exact; low = bf16(x · A_e)."""
+def test_the_fp8_activation_pass_is_bit_exact(K, colscale, terms):
+    """mlora_fp8_prep against the oracle: e4m3 bytes (one term, or hi and lo) and E8M0 scales bit-exact;
+    low = bf16(x · A_e)."""
     from meepsquared_amd import _lib
 
     torch.manual_seed(K)
@@ -343,17 +349,17 @@ def test_the_fp8_activation_pass_is_bit_exact(K, colscale):
     at = (torch.randn(E, R, K) * 0.1).bfloat16().cuda()
     cs = (torch.rand(E, K) + 0.5).cuda() if colscale else None
     nkb = (K + 63) // 64
-    x8 = torch.empty(rows, nkb * 64, dtype=torch.uint8, device="cuda")
+    x8 = torch.empty(rows, terms * nkb * 64, dtype=torch.uint8, device="cuda")
     xs = torch.empty(nkb, rows, dtype=torch.int32, device="cuda")
     low = torch.empty(rows, R, dtype=torch.bfloat16, device="cuda")
-    _lib.call("mlora_fp8_prep", _lib.ptr(x), x.stride(0), rows, K, _lib.ptr(cs), cs.stride(0) if cs is not None else 0,
+    _lib.call("mlora_fp8_prep", _lib.ptr(x), x.stride(0), rows, K, terms, _lib.ptr(cs), cs.stride(0) if cs is not None else 0,
               _lib.ptr(x8), x8.stride(0), _lib.ptr(xs), xs.stride(0), _lib.ptr(at), at.stride(0), at.stride(1), R,
               _lib.ptr(low), low.stride(0), _lib.ptr(offsets), E, _lib.stream())
     torch.cuda.synchronize()
     expert = torch.repeat_interleave(torch.arange(E), torch.tensor(counts))
     xc = x.float().cpu()
     scaled = xc * cs.cpu()[expert] if colscale else xc
-    q, e8 = formats.fp8_rows_quantize(scaled)
+    q, e8 = formats.fp8_rows_quantize(scaled) if terms == 1 else formats.fp8_rows_quantize2(scaled)
     assert torch.equal(x8.cpu(), q)
     assert torch.equal(xs.cpu(), e8)
     low_ref = torch.einsum("rk,rjk->rj", xc.double(), at.cpu().double()[expert]).float()
