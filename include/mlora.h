@@ -155,14 +155,21 @@ int mlora_grouped_gemm_gather(const void* x, int64_t ldx, int64_t x_rows, const 
                               const void* bias, int64_t bias_se, void* out, int64_t ldo, void* low, int64_t ldl,
                               const int32_t* offsets, int E, void* stream);
 
+/* Scratch bytes mlora_grouped_reduce(_gather) needs for (rows, N, R, E): the partial sums of split
+ * experts (16-byte aligned, contents on entry ignored); 0 when no expert can be split (E > 32). */
+size_t mlora_grouped_reduce_workspace_bytes(int64_t rows, int N, int R, int E);
+
 /* out[e, n, r] = bf16(scaling · sum over expert e's rows of g[row, n] · l[row, r]), fp32
  * accumulation in a fixed order, no atomics: the adapters' gradients.  g (rows, N) bf16 row stride
  * ldg; l (rows, R) bf16 row stride ldl; out addressed out[e*o_se + n*o_sn + r*o_sr].  R <= 64,
- * rows < 2^32.
+ * rows < 2^32.  With E <= 32 an expert with more rows than a part (max(4096, the mean rows per expert
+ * rounded up to a power of two)) is summed in parts whose fp32 partial sums go through the workspace and
+ * are added in part order by a second launch.
  * Replaces _grouped_reduce_kernel (src/meepsquared/_grouped.py:232-256). */
 int mlora_grouped_reduce(const void* g, int64_t ldg, const void* l, int64_t ldl, int64_t rows, int N, int R,
                          float scaling, const int32_t* offsets, int E,
-                         void* out, int64_t o_se, int64_t o_sn, int64_t o_sr, void* stream);
+                         void* out, int64_t o_se, int64_t o_sn, int64_t o_sr, void* workspace, size_t workspace_bytes,
+                         void* stream);
 
 /* mlora_grouped_reduce with the rows of g gathered and/or weighted: with gather, row r is row
  * gather[r] / k of g (A's gradient of the gate_up product when its input rows are gathered, as
@@ -173,7 +180,8 @@ int mlora_grouped_reduce(const void* g, int64_t ldg, const void* l, int64_t ldl,
 int mlora_grouped_reduce_gather(const void* g, int64_t ldg, const int64_t* gather, int k, const void* row_scale,
                                 int row_scale_dtype, const int64_t* scale_index, const void* l, int64_t ldl,
                                 int64_t rows, int N, int R, float scaling, const int32_t* offsets, int E,
-                                void* out, int64_t o_se, int64_t o_sn, int64_t o_sr, void* stream);
+                                void* out, int64_t o_se, int64_t o_sn, int64_t o_sr, void* workspace,
+                                size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------------------------
  * The layer around the products: gather, SwiGLU, combine (bf16 activations)

@@ -362,17 +362,21 @@ def _reduce(g: torch.Tensor, low: torch.Tensor, offsets: torch.Tensor, scaling: 
     if rows == 0:  # a sum over no rows (an empty gather or scale index has no device pointer to pass)
         return out.zero_()
     info = {"rows": rows, "N": N, "R": R, "gathered": gather is not None, "scaled": row_scale is not None}
+    ws = torch.empty(int(_lib.lib.mlora_grouped_reduce_workspace_bytes(rows, N, R, experts)), device=g.device,
+                     dtype=torch.uint8)
     if launch_observer is not None:
         launch_observer("grouped_reduce", "before", info)
     if gather is None and row_scale is None:
         call("mlora_grouped_reduce", ptr(g), g.stride(0), ptr(low), low.stride(0), rows, N, R, float(scaling),
-             ptr(offsets), experts, ptr(out), o_se, o_sn, o_sr, _lib.stream(g.device))
+             ptr(offsets), experts, ptr(out), o_se, o_sn, o_sr, ptr(ws) if ws.numel() else None, ws.numel(),
+             _lib.stream(g.device))
     else:
         perm, k = gather if gather is not None else (None, 1)
         w, index = row_scale if row_scale is not None else (None, None)
         call("mlora_grouped_reduce_gather", ptr(g), g.stride(0), ptr(perm), k, ptr(w),
              _lib.dtype_code(w.dtype) if w is not None else 0, ptr(index), ptr(low), low.stride(0), rows, N, R,
-             float(scaling), ptr(offsets), experts, ptr(out), o_se, o_sn, o_sr, _lib.stream(g.device))
+             float(scaling), ptr(offsets), experts, ptr(out), o_se, o_sn, o_sr, ptr(ws) if ws.numel() else None,
+             ws.numel(), _lib.stream(g.device))
     if launch_observer is not None:
         launch_observer("grouped_reduce", "after", info)
     return out

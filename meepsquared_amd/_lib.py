@@ -40,9 +40,11 @@ SIGNATURES = {
     "mlora_grouped_gemm_gather": (c_int, [P, I64, I64, P, c_int, P, c_int, I64, c_int, c_int, P, c_int, I64, I64, I64,
                                           P, c_int, I64, P, I64, I64, P, I64, I64, c_int, c_float, P, I64,
                                           P, I64, P, I64, P, c_int, P]),
-    "mlora_grouped_reduce": (c_int, [P, I64, P, I64, I64, c_int, c_int, c_float, P, c_int, P, I64, I64, I64, P]),
+    "mlora_grouped_reduce_workspace_bytes": (c_size_t, [I64, c_int, c_int, c_int]),
+    "mlora_grouped_reduce": (c_int, [P, I64, P, I64, I64, c_int, c_int, c_float, P, c_int, P, I64, I64, I64, P, c_size_t,
+                                     P]),
     "mlora_grouped_reduce_gather": (c_int, [P, I64, P, c_int, P, c_int, P, P, I64, I64, c_int, c_int, c_float, P,
-                                            c_int, P, I64, I64, I64, P]),
+                                            c_int, P, I64, I64, I64, P, c_size_t, P]),
     "mlora_gather_rows": (c_int, [P, I64, I64, P, I64, c_int, P, c_int, P, P]),
     "mlora_gather_rows_backward": (c_int, [P, I64, P, I64, c_int, P, c_int, P, P]),
     "mlora_swiglu": (c_int, [P, I64, I64, P, P]),

@@ -15,6 +15,15 @@
 // Rows of g may be gathered (row r read from g[gather[r] / gk]) and weighted by a per-row scale,
 // applied to the narrow operand: row r of l taken as bf16(row_scale[scale_index[r]] · l[r]).
 //
+// With few experts (E <= 32), an expert's rows are cut into parts of at most P rows (P = part_rows(rows,
+// E): at least 4096, and at least the mean rows per expert), one workgroup per (part, 64 columns), so that
+// an expert holding a large share of the rows (Zipf routing) is spread over many workgroups instead of
+// bounding the launch; with more experts each holds a small share and P covers every expert.  Part p of
+// expert e is grid row e + floor(start_e / P) + p (an injective map, so no scan of the experts is needed;
+// grid rows that map to no part exit at once).  A single-part expert's workgroup writes its result; a
+// split expert's parts write fp32 partial sums to the workspace and reduce_finish_kernel, the next launch,
+// adds them in part order: deterministic.
+//
 // Reference behaviour: src/meepsquared/_grouped.py:232-256 (_grouped_reduce_kernel), :362-370 (_reduce).
 #include "common.hpp"
 
@@ -26,6 +35,24 @@ constexpr int RB_WAVES = 4;   // waves per workgroup
 constexpr int RB_IB = 1024;  // rows whose indices are staged in LDS at a time
 constexpr int RB_P = RB_CH + 8;  // LDS pitch of the transposed tiles in bf16 (80 bytes: the MFMA
                                  // operand reads of 16 lanes cover the 64 banks once)
+constexpr int RB_MIN_PART = 4096;  // rows per part at least
+constexpr int RB_SPLIT_E = 32;     // experts up to which an expert's rows are split into parts
+
+// rows per part: with up to RB_SPLIT_E experts a power of two, at least RB_MIN_PART and the mean rows per
+// expert (balanced routing splits nothing; a skewed expert splits into a few parts); else all the rows
+__host__ __device__ inline int64_t part_rows(int64_t rows, int E) {
+  if (E > RB_SPLIT_E) return rows > 0 ? rows : 1;
+  const int64_t mean = (rows + E - 1) / E;
+  int64_t p = RB_MIN_PART;
+  while (p < mean) p <<= 1;
+  return p;
+}
+// grid rows: expert e's parts at e + floor(start_e / P) + p, all below E + rows / P + 1
+__host__ __device__ inline int64_t part_slots(int64_t rows, int E) { return rows / part_rows(rows, E) + E + 1; }
+
+__device__ __forceinline__ int64_t expert_start(const int32_t* offsets, int64_t rows, int e) {
+  return e == 0 ? 0 : min(max((int64_t)offsets[e - 1], (int64_t)0), rows);
+}
 
 __device__ __forceinline__ uint32_t lo2(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x05040100u); }
 __device__ __forceinline__ uint32_t hi2(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x07060302u); }
@@ -48,6 +75,7 @@ __global__ __launch_bounds__(256) void grouped_reduce_kernel(const bf16* __restr
                                                              const int64_t* __restrict__ rs_idx,
                                                              const bf16* __restrict__ l, int64_t ldl, int64_t rows,
                                                              int N, float scaling, const int32_t* __restrict__ offsets,
+                                                             int E, int64_t P, float* __restrict__ partial,
                                                              bf16* __restrict__ out, int64_t o_se, int64_t o_sn,
                                                              int64_t o_sr) {
   constexpr int R = NRB * 16;
@@ -58,15 +86,37 @@ __global__ __launch_bounds__(256) void grouped_reduce_kernel(const bf16* __restr
   __shared__ uint32_t Is[GATHER ? RB_IB : 1];
   __shared__ uint32_t Ss[SCALED ? RB_IB : 1];
   static_assert(RB_WAVES * RB_N * RB_P * 2 >= RB_WAVES * RB_N * 16 * 4, "the partial sums fit in Gs");
-  // gathered rows: consecutive workgroups take consecutive column blocks of one expert, so the rows
-  // they read at once are whole rows of the source; the expert's own rows: consecutive workgroups
-  // take consecutive experts
-  const int e = GATHER ? blockIdx.y : blockIdx.x;
-  const int n0 = (GATHER ? blockIdx.x : blockIdx.y) * RB_N;
+  // Split experts, or gathered rows: consecutive workgroups take consecutive column blocks of one part,
+  // so the rows they read at once are whole rows of the source, and parts run in expert order (a split
+  // expert starts early).  Otherwise one part per expert and consecutive workgroups take consecutive
+  // experts (grid x: the expert).
+  const bool whole = P >= rows;  // every expert is one part: grid row = expert
+  const bool by_expert = whole && !GATHER;
+  const int slot = by_expert ? blockIdx.x : blockIdx.y;
+  const int nbk = by_expert ? blockIdx.y : blockIdx.x;
+  const int nblk = (N + RB_N - 1) / RB_N;
+  const int n0 = nbk * RB_N;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: the chunk loop is a scalar loop
-  const int64_t start = e == 0 ? 0 : min(max((int64_t)offsets[e - 1], (int64_t)0), rows);
-  const int64_t end = min(max((int64_t)offsets[e], (int64_t)0), rows);
+  auto base = [&](int x) { return (int64_t)x + expert_start(offsets, rows, x) / P; };
+  int e;
+  if (whole) {
+    if (slot >= E) return;
+    e = slot;
+  } else {
+    int lo = 0, hi = E - 1;  // the last expert whose first part's row is at or before this one
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (base(mid) <= slot) lo = mid; else hi = mid - 1;
+    }
+    e = __builtin_amdgcn_readfirstlane(lo);
+  }
+  const int64_t estart = expert_start(offsets, rows, e), eend = expert_start(offsets, rows, e + 1);
+  const int np = eend > estart ? (int)((eend - estart + P - 1) / P) : 1;  // an empty expert: one part of zeros
+  const int part = whole ? 0 : slot - (int)base(e);
+  if (part >= np) return;  // a grid row between two experts' parts
+  const int64_t start = min(eend, estart + (int64_t)part * P);
+  const int64_t end = min(eend, start + P);
 
   const int gq = (lane >> 3) * 4, gc = (lane & 7) * 8;
   const bool g_cols = n0 + gc < N;
@@ -208,8 +258,32 @@ __global__ __launch_bounds__(256) void grouped_reduce_kernel(const bf16* __restr
 #pragma unroll
       for (int w = 1; w < RB_WAVES; ++w) s += red[w * RB_N * 16 + idx];
       const int n = n0 + col;
-      if (n < N) out[(int64_t)e * o_se + (int64_t)n * o_sn + (int64_t)(j * 16 + r) * o_sr] = (bf16)(s * scaling);
+      if (np == 1) {
+        if (n < N) out[(int64_t)e * o_se + (int64_t)n * o_sn + (int64_t)(j * 16 + r) * o_sr] = (bf16)(s * scaling);
+      } else {  // a split expert: this part's sums, [grid row][column block][64][R]
+        partial[(((int64_t)slot * nblk + nbk) * RB_N + col) * R + j * 16 + r] = s;
+      }
     }
+  }
+}
+
+// The parts of each split expert added in part order, scaled and rounded: one workgroup per (64 columns,
+// expert); a single-part expert's result is written already.
+__global__ __launch_bounds__(256) void reduce_finish_kernel(const float* __restrict__ partial,
+                                                            const int32_t* __restrict__ offsets, int64_t rows, int E,
+                                                            int64_t P, int N, int R, float scaling,
+                                                            bf16* __restrict__ out, int64_t o_se, int64_t o_sn,
+                                                            int64_t o_sr) {
+  const int e = blockIdx.y, nb = blockIdx.x, nblk = gridDim.x;
+  const int64_t estart = expert_start(offsets, rows, e), eend = expert_start(offsets, rows, e + 1);
+  const int np = eend > estart ? (int)((eend - estart + P - 1) / P) : 1;
+  if (np <= 1) return;
+  const int64_t s0 = (int64_t)e + estart / P;
+  for (int idx = threadIdx.x; idx < RB_N * R; idx += 256) {
+    const int col = idx / R, r = idx - col * R, n = nb * RB_N + col;
+    float sum = 0.f;
+    for (int q = 0; q < np; ++q) sum += partial[((s0 + q) * nblk + nb) * RB_N * R + idx];
+    if (n < N) out[(int64_t)e * o_se + (int64_t)n * o_sn + (int64_t)r * o_sr] = (bf16)(sum * scaling);
   }
 }
 
@@ -217,10 +291,16 @@ __global__ __launch_bounds__(256) void grouped_reduce_kernel(const bf16* __restr
 
 using namespace mlora;
 
+extern "C" size_t mlora_grouped_reduce_workspace_bytes(int64_t rows, int N, int R, int E) {
+  if (rows < 0 || E < 1 || N < 1 || R < 1 || rows <= part_rows(rows, E)) return 0;  // no expert can be split
+  const int64_t nblk = (N + RB_N - 1) / RB_N;
+  return (size_t)part_slots(rows, E) * (size_t)nblk * RB_N * (size_t)R * sizeof(float);
+}
+
 static int grouped_reduce_impl(const void* g, int64_t ldg, const int64_t* gather, int gk, const void* row_scale,
                                int rs_dt, const int64_t* rs_idx, const void* l, int64_t ldl, int64_t rows, int N, int R,
                                float scaling, const int32_t* offsets, int E, void* out, int64_t o_se, int64_t o_sn,
-                               int64_t o_sr, void* stream) {
+                               int64_t o_sr, void* workspace, size_t workspace_bytes, void* stream) {
   clear_error();
   if (gather != nullptr && gk < 1) return fail("grouped_reduce_gather: k=%d must be >= 1", gk);
   if (row_scale != nullptr && (rs_idx == nullptr || (rs_dt != MLORA_DT_BF16 && rs_dt != MLORA_DT_F32)))
@@ -231,12 +311,20 @@ static int grouped_reduce_impl(const void* g, int64_t ldg, const int64_t* gather
     return fail("grouped_reduce: g needs N (%d) and its row stride (%lld) multiples of 8, 16-byte aligned", N, (long long)ldg);
   if (R < 16 || R > 64 || R % 16) return fail("grouped_reduce: R=%d must be 16, 32, 48 or 64", R);
   if (ldl < R || ldl % 8 || ((uintptr_t)l & 15u)) return fail("grouped_reduce: l needs 16-byte aligned rows of >= R values");
+  const size_t need = mlora_grouped_reduce_workspace_bytes(rows, N, R, E);
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need || ((uintptr_t)workspace & 15u)))
+    return fail("grouped_reduce: workspace of %zu bytes, %zu needed (16-byte aligned)", workspace_bytes, need);
   const unsigned nblk = (unsigned)((N + RB_N - 1) / RB_N);
-  const dim3 grid(gather != nullptr ? nblk : (unsigned)E, gather != nullptr ? (unsigned)E : nblk), block(256);
+  const int64_t P = part_rows(rows, E), slots = part_slots(rows, E);
+  if (slots > 65535) return fail("grouped_reduce: %lld grid rows past the grid's 65535", (long long)slots);
+  // one part per expert and rows not gathered: the expert is grid x (consecutive workgroups, consecutive experts)
+  const bool by_expert = P >= rows && gather == nullptr;
+  const dim3 grid(by_expert ? (unsigned)slots : nblk, by_expert ? nblk : (unsigned)slots), block(256);
   hipStream_t s = as_stream(stream);
 #define MLORA_RED(NRB, GA, SC)                                                                                       \
   hipLaunchKernelGGL((grouped_reduce_kernel<NRB, GA, SC>), grid, block, 0, s, (const bf16*)g, ldg, gather, gk, row_scale, \
-                     rs_dt, rs_idx, (const bf16*)l, ldl, rows, N, scaling, offsets, (bf16*)out, o_se, o_sn, o_sr)
+                     rs_dt, rs_idx, (const bf16*)l, ldl, rows, N, scaling, offsets, E, P, (float*)workspace,         \
+                     (bf16*)out, o_se, o_sn, o_sr)
 #define MLORA_RED_R(GA, SC)            \
   switch (R / 16) {                    \
     case 1: MLORA_RED(1, GA, SC); break; \
@@ -250,25 +338,32 @@ static int grouped_reduce_impl(const void* g, int64_t ldg, const int64_t* gather
   else MLORA_RED_R(false, false)
 #undef MLORA_RED_R
 #undef MLORA_RED
-  return launch_status("grouped_reduce");
+  if (int rc = launch_status("grouped_reduce")) return rc;
+  if (need > 0) {  // some expert may have been split
+    hipLaunchKernelGGL(reduce_finish_kernel, dim3(nblk, (unsigned)E), dim3(256), 0, s, (const float*)workspace, offsets,
+                       rows, E, P, N, R, scaling, (bf16*)out, o_se, o_sn, o_sr);
+    return launch_status("grouped_reduce/finish");
+  }
+  return 0;
 }
 
 extern "C" int mlora_grouped_reduce(const void* g, int64_t ldg, const void* l, int64_t ldl, int64_t rows, int N, int R,
                                     float scaling, const int32_t* offsets, int E, void* out, int64_t o_se,
-                                    int64_t o_sn, int64_t o_sr, void* stream) {
+                                    int64_t o_sn, int64_t o_sr, void* workspace, size_t workspace_bytes,
+                                    void* stream) {
   return grouped_reduce_impl(g, ldg, nullptr, 1, nullptr, 0, nullptr, l, ldl, rows, N, R, scaling, offsets, E, out,
-                             o_se, o_sn, o_sr, stream);
+                             o_se, o_sn, o_sr, workspace, workspace_bytes, stream);
 }
 
 extern "C" int mlora_grouped_reduce_gather(const void* g, int64_t ldg, const int64_t* gather, int k,
                                            const void* row_scale, int row_scale_dtype, const int64_t* scale_index,
                                            const void* l, int64_t ldl, int64_t rows, int N, int R, float scaling,
                                            const int32_t* offsets, int E, void* out, int64_t o_se, int64_t o_sn,
-                                           int64_t o_sr, void* stream) {
+                                           int64_t o_sr, void* workspace, size_t workspace_bytes, void* stream) {
   if (gather == nullptr && row_scale == nullptr) {
     clear_error();
     return fail("grouped_reduce_gather: neither gather nor a row scale");
   }
   return grouped_reduce_impl(g, ldg, gather, k, row_scale, row_scale_dtype, scale_index, l, ldl, rows, N, R, scaling,
-                             offsets, E, out, o_se, o_sn, o_sr, stream);
+                             offsets, E, out, o_se, o_sn, o_sr, workspace, workspace_bytes, stream);
 }

@@ -86,32 +86,35 @@ constexpr int kTopkMaxE = 1024;
 // Entries are codes rank << 8 | list position (rank: the first selection round that took this value,
 // so a smaller rank is a larger value); an empty position has rank 0xFF.
 constexpr int kTieNet = 32;
-__device__ __forceinline__ void tie_cmpx(uint32_t& a, uint32_t& b, bool flag) {
-  const uint32_t ra = a >> 8, rb = b >> 8;
-  const bool swap = ra < rb || rb == 0xFFu;  // an empty a has the largest rank, so ra < rb implies a present
-  if (swap == flag) {
-    const uint32_t t = a;
-    a = b;
-    b = t;
-  }
-}
-__device__ __forceinline__ void tie_network(uint32_t (&c)[kTieNet]) {
+
+// The network run by a token's L lanes on the 32 positions, position i = lane + L·q held in c[q]: at each
+// compare-exchange stage (merge size `size`, distance `stride`) position i meets i ^ stride — in this lane's
+// other slot when stride >= L, else in lane ^ stride — and both keep the same one of the pair.  The pair's
+// direction flag is bit `size` of its positions (false in the final merge).
+template <int L>
+__device__ __forceinline__ void tie_network(uint32_t (&c)[L >= kTieNet ? 1 : kTieNet / L], int gl) {
+  constexpr int NQ = L >= kTieNet ? 1 : kTieNet / L;
+  auto stage = [&](int size, int stride) {
+    uint32_t other[NQ];
+#pragma unroll
+    for (int q = 0; q < NQ; ++q)
+      other[q] = stride >= L ? c[q ^ (stride / L)] : (uint32_t)__shfl_xor((int)c[q], stride, kWave);
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      const int i = gl + L * q;
+      const bool lower = (i & stride) == 0;
+      const uint32_t a = lower ? c[q] : other[q], b = lower ? other[q] : c[q];
+      const bool swap = (a >> 8) < (b >> 8) || (b >> 8) == 0xFFu;  // a above b (so present), or b empty
+      const bool flag = size < kTieNet && (i & size) != 0;
+      if (swap == flag) c[q] = other[q];
+    }
+  };
 #pragma unroll
   for (int size = 2; size < kTieNet; size *= 2)
 #pragma unroll
-    for (int stride = size / 2; stride > 0; stride /= 2)
+    for (int stride = size / 2; stride > 0; stride /= 2) stage(size, stride);
 #pragma unroll
-      for (int q = 0; q < kTieNet / 2; ++q) {
-        const int a = 2 * q - (q & (stride - 1));
-        tie_cmpx(c[a], c[a + stride], (q & (size / 2)) != 0);
-      }
-#pragma unroll
-  for (int stride = kTieNet / 2; stride > 0; stride /= 2)
-#pragma unroll
-    for (int q = 0; q < kTieNet / 2; ++q) {
-      const int a = 2 * q - (q & (stride - 1));
-      tie_cmpx(c[a], c[a + stride], false);
-    }
+  for (int stride = kTieNet / 2; stride > 0; stride /= 2) stage(kTieNet, stride);
 }
 
 template <typename TL, typename TW, int L, int PL>
@@ -230,14 +233,23 @@ __global__ __launch_bounds__(256) void topk_softmax_kernel(const TL* __restrict_
       }
     }
     __syncthreads();
-    if (wave_live && gl == 0) {
-      uint32_t c[kTieNet];
+    constexpr int NQ = L >= kTieNet ? 1 : kTieNet / L;
+    uint32_t c[NQ];
+    if (wave_live) {  // every lane of a live wave: the network exchanges values between lanes
 #pragma unroll
-      for (int q = 0; q < kTieNet; ++q) c[q] = q < k ? s_code[tok][q] : 0xFFFFu;
-      tie_network(c);
+      for (int q = 0; q < NQ; ++q) {
+        const int i = gl + L * q;
+        c[q] = i < k ? s_code[tok][i] : 0xFFFFu;  // (k <= 32: positions past 31 are always empty)
+      }
+      tie_network<L>(c, gl);
+    }
+    __syncthreads();  // every read of the gather order is done before it is overwritten
+    if (wave_live) {
 #pragma unroll
-      for (int q = 0; q < kTieNet; ++q)
-        if (q < k) s_code[tok][q] = c[q] & 0xFFu;  // output q takes list position c[q] & 0xFF
+      for (int q = 0; q < NQ; ++q) {
+        const int i = gl + L * q;
+        if (i < k) s_code[tok][i] = c[q] & 0xFFu;  // output i takes list position c[q] & 0xFF
+      }
     }
     __syncthreads();
   }
