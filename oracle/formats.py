@@ -114,6 +114,26 @@ def fp8_rows_dequantize2(q, words, K):
     return (hi + lo)[:, :K]
 
 
+def fp8_tensor_quantize(w):
+    """(q e4m3, scale 0-d fp32): one scale for the whole tensor — src/meepsquared/_fp8.py:95-109 (its CPU
+    branch, :106-108), scale = max(amax, 1e-12) / 448.
+    Pinned by: fp8_quantize over one expert (the same rule, pinned by torch's e4m3 cast), and the
+    round-trip bound of tests/test_fp8.py:122-131 (tests/test_oracle.py)."""
+    w = torch.as_tensor(w).float()
+    scale = torch.clamp(w.abs().amax(), min=1e-12) / E4M3_MAX
+    return (w / scale).to(torch.float8_e4m3fn), scale
+
+
+def fp8_scaled_mm(x, weight8, weight_scale, transpose_weight, bias=None):
+    """x @ W^T (transpose_weight) or x @ W with W = weight8 · weight_scale, in float32 — the reference's
+    own CPU path of scaled_mm (src/meepsquared/_fp8.py:205-207), without its final bf16 cast; bias added.
+    Pinned by: a diagonal weight (x times the diagonal, a closed form) and the transpose identity
+    (x @ W^T)^T = W @ x^T (tests/test_oracle.py)."""
+    w = torch.as_tensor(weight8).float() * torch.as_tensor(weight_scale).float()
+    y = torch.as_tensor(x).float() @ (w.t() if transpose_weight else w)
+    return y if bias is None else y + torch.as_tensor(bias).float()
+
+
 def nf4_code_from_definition():
     """The 16 NF4 values from QLoRA's definition (Dettmers et al. 2023, Appendix E): 8 positive
     quantiles of N(0,1) from the upper half (offset 0.9677 = 1/2 (1/(2·15) + 1/(2·16)) mapped to

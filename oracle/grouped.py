@@ -77,3 +77,25 @@ def reference_lora_bf16_low(x, weight, scale, offsets, is_transposed, lhs, rhs, 
         out.append(y)
         start = end
     return torch.cat(out)
+
+
+def lora_mlp_swiglu(x, gate, up, down, biases=(None, None, None)):
+    """The dense SwiGLU MLP with LoRA on each projection, float32, differentiable — the forward of
+    src/meepsquared/_vendor/axolotl/lora.py:398-830 (LoRA_MLP, no dropout, no DoRA): each projection
+    (W (out, in), A (r, in) or None, B (out, r), s) as reference_lora over one expert, then
+    silu(gate) · up.
+    Pinned by: reference_lora (pinned above) and the SwiGLU oracle (tests/test_oracle.py)."""
+    from oracle.moe import swiglu
+
+    rows = x.shape[0]
+    offsets = [rows]
+
+    def proj(h, p, b):
+        w, a, bb, s = p
+        return reference_lora(h, w.float().unsqueeze(0), None, offsets, False,
+                              None if a is None else bb.float().unsqueeze(0), None if a is None else a.float().unsqueeze(0),
+                              s, None if b is None else b.float().unsqueeze(0), out_dtype=torch.float32)
+
+    g = proj(x.float(), gate, biases[0])
+    u = proj(x.float(), up, biases[1])
+    return proj(swiglu(torch.cat([g, u], dim=-1)), down, biases[2])

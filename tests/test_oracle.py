@@ -341,3 +341,43 @@ def test_fp8_two_term_quantisation_is_hi_plus_the_quantised_exact_residual():
         assert torch.all((rec - x)[:, blk].abs().amax(dim=1) <= amax * 2.0 ** -7)
     one = formats.fp8_rows_dequantize(hi1, e1, 200)
     assert (rec - x).norm() < (one - x).norm() / 8  # the second term buys at least 3 bits
+
+
+def test_dense_fp8_oracle_closed_forms():
+    """fp8_tensor_quantize is fp8_quantize over one expert and keeps the reference's round-trip bound;
+    fp8_scaled_mm of a diagonal weight scales x's columns; x @ W^T is (W @ x^T)^T; x @ W uses W untransposed."""
+    torch.manual_seed(5)
+    w = torch.randn(48, 32) * 0.3
+    q, s = formats.fp8_tensor_quantize(w)
+    q1, s1 = formats.fp8_quantize(w.unsqueeze(0))
+    assert torch.equal(q.view(torch.uint8), q1[0].view(torch.uint8)) and torch.equal(s.reshape(1), s1)
+    assert (q.float() * s - w).abs().max() <= 0.07 * w.abs().max()  # tests/test_fp8.py:122-131
+    d = torch.tensor([1.0, 2.0, 0.5, -4.0, 0.25, 3.0, -1.0, 8.0])
+    dq, ds = formats.fp8_tensor_quantize(torch.diag(d))
+    x = torch.randn(5, 8)
+    assert torch.allclose(formats.fp8_scaled_mm(x, dq, ds, True), x * (dq.float().diagonal() * ds), atol=1e-6)
+    x = torch.randn(7, 32)
+    y = formats.fp8_scaled_mm(x, q, s, True, bias=torch.ones(48))
+    assert torch.allclose(y - 1, ((q.float() * s) @ x.t()).t(), atol=1e-5)
+    g = torch.randn(7, 48)
+    assert torch.allclose(formats.fp8_scaled_mm(g, q, s, False), g @ (q.float() * s), atol=1e-5)
+
+
+def test_lora_mlp_oracle_equals_the_merged_weight_mlp():
+    """oracle.grouped.lora_mlp_swiglu against the MLP on merged weights W + s·B·A in float64 (a different
+    formulation: the adapters folded into the weights before the products)."""
+    torch.manual_seed(6)
+    H, I, r = 24, 40, 4
+    def p(o, i, s):
+        return torch.randn(o, i) * 0.1, torch.randn(r, i) * 0.2, torch.randn(o, r) * 0.2, s
+    gate, up, down = p(I, H, 2.0), p(I, H, 0.5), p(H, I, 1.5)
+    bias = (torch.randn(I), None, torch.randn(H))
+    x = torch.randn(9, H)
+    got = grouped.lora_mlp_swiglu(x, gate, up, down, bias)
+    def merged(t):
+        w, a, b, s = t
+        return (w.double() + s * b.double() @ a.double())
+    g = x.double() @ merged(gate).t() + bias[0].double()
+    u = x.double() @ merged(up).t()
+    want = (torch.nn.functional.silu(g) * u) @ merged(down).t() + bias[2].double()
+    assert torch.allclose(got.double(), want, rtol=1e-4, atol=1e-5)
