@@ -84,6 +84,10 @@ __device__ __forceinline__ int swz_kn(int k, int chunk) { return k * BN + ((chun
 __device__ __forceinline__ void dma16(rsrc_t r, const bf16* lds_dst, uint32_t voff) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)lds_dst, 16, voff, 0, 0, 0);
 }
+// the same with a wave-uniform scalar offset added to the lane's
+__device__ __forceinline__ void dma16s(rsrc_t r, const bf16* lds_dst, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)lds_dst, 16, voff, __builtin_amdgcn_readfirstlane(soff), 0, 0);
+}
 
 // s_waitcnt vmcnt(N) with expcnt and lgkmcnt left free
 template <int N>
@@ -217,8 +221,11 @@ struct SlotSize {
   static constexpr int kElems = kXOff + (TALL ? XR * BK : 0);
 };
 
-// Per-lane DMA addressing of one item, fixed for its whole K loop: byte offsets at k = 0 and the
-// k of each lane's chunk (a huge k marks a column past N: never in range).
+// Per-lane DMA addressing of one item, fixed for its whole K loop: each lane's byte offsets at k = 0.
+// A stage that lies wholly inside K (every stage when K is a multiple of BK) adds its k offset as the
+// copy's scalar offset, with no per-lane test; only a stage that crosses the end of K re-derives each
+// lane's k from its lane index and sends the lanes past K out of range (zeros).  Stack columns past N
+// are read like the others (inside the stack's buffer range, or zeros past its end) and never stored.
 template <bool BKC, int NRB, int WT, bool TALL = false>
 struct Feed {
   static_assert(WT == kWBf16 || BKC, "fp8 and NF4 stacks are read with k contiguous");
@@ -235,14 +242,41 @@ struct Feed {
   static constexpr int kTallWaves = XR * CPR / 64;
   static_assert(!TALL || (STAGES == 2 && (XR * CPR) % 64 == 0 && kTallWaves <= NW), "tall rows' copies");
   uint32_t to;
-  int tk, td;
+  int td;
   bool t_on;
   uint32_t xo[XI], wo[WI], ao;
-  int xk[XI], wk[WI], ak;
   int xd[XI], wd[WI], ad;  // LDS element offset of each instruction's 64 lanes within the slot
   bool a_on;
   int lane_, wave_, n0_;
   int64_t wstep;           // bytes the stack offset advances per k (BKC: 2; else 2 * w_sk)
+
+  // the k (within a stage) of this lane's chunk in copy q of the x tile, the stack tile, the A^T tile
+  // and the tall rows' tile
+  __device__ __forceinline__ static int x_k(int wave, int q, int lane) {
+    const int ci = (wave * XI + q) * 64 + lane, row = ci / CPR;
+    return ((ci % CPR) ^ swz_f(row)) * 8;
+  }
+  __device__ __forceinline__ static int w_k(int wave, int q, int lane) {
+    const int ci = (wave * WI + q) * 64 + lane;
+    if constexpr (WT != kWBf16) {
+      constexpr int CH = WTile<WT>::Chunks;
+      const int row = ci / CH;
+      return ((ci % CH) ^ swz_q<WT>(row)) * (WTile<WT>::kFp8 ? 16 : 32);
+    } else if constexpr (BKC) {
+      const int row = ci / CPR;
+      return ((ci % CPR) ^ swz_f(row)) * 8;
+    } else {
+      return ci / (BN / 8);
+    }
+  }
+  __device__ __forceinline__ static int a_k(int wave, int lane) {
+    const int ci = ((wave * CPW) >> 6) * 64 + lane, r = ci / CPR;
+    return ((ci % CPR) ^ swz_f(r)) * 8;
+  }
+  __device__ __forceinline__ static int t_k(int wave, int lane) {
+    const int ci = wave * 64 + lane, row = ci / CPR;
+    return ((ci % CPR) ^ swz_f(row)) * 8;
+  }
 
   __device__ __forceinline__ void init(const GemmArgs& p, int n0, int64_t row0, int mrows, int wave, int lane) {
     lane_ = lane;
@@ -259,7 +293,6 @@ struct Feed {
         const int64_t src = row < mrows ? (int64_t)((uint32_t)p.gather[row0 + row] / (uint32_t)p.gk) : -1;
         xo[q] = src >= 0 ? (uint32_t)((src * p.ldx + c * 8) * 2) : kOob;
       }
-      xk[q] = c * 8;
       xd[q] = instr * 512;
     }
 #pragma unroll
@@ -270,18 +303,15 @@ struct Feed {
         const int row = ci / CH, c = (ci % CH) ^ swz_q<WT>(row);
         const int n = n0 + row;
         const int64_t rowb = WTile<WT>::kFp8 ? (int64_t)n * p.w_sn : (int64_t)n * p.w_sn / 2;
-        wo[q] = n < p.N ? (uint32_t)(rowb + c * 16) : 0u;
-        wk[q] = n < p.N ? c * (WTile<WT>::kFp8 ? 16 : 32) : (1 << 30);
+        wo[q] = (uint32_t)(rowb + c * 16);
       } else if constexpr (BKC) {  // [n][k]
         const int row = ci / CPR, c = (ci % CPR) ^ swz_f(row);
         const int n = n0 + row;
-        wo[q] = n < p.N ? (uint32_t)(((int64_t)n * p.w_sn + c * 8) * 2) : 0u;
-        wk[q] = n < p.N ? c * 8 : (1 << 30);
+        wo[q] = (uint32_t)(((int64_t)n * p.w_sn + c * 8) * 2);
       } else {  // [k][n]
         const int kr = ci / (BN / 8), c = (ci % (BN / 8)) ^ ((kr & 3) << 2);
         const int n = n0 + c * 8;
-        wo[q] = n < p.N ? (uint32_t)(((int64_t)kr * p.w_sk + n) * 2) : 0u;
-        wk[q] = n < p.N ? kr : (1 << 30);
+        wo[q] = (uint32_t)(((int64_t)kr * p.w_sk + n) * 2);
       }
       wd[q] = BM * BK + instr * 512;
     }
@@ -295,7 +325,6 @@ struct Feed {
         const int64_t src = BM + row < mrows ? (int64_t)((uint32_t)p.gather[row0 + BM + row] / (uint32_t)p.gk) : -1;
         to = src >= 0 ? (uint32_t)((src * p.ldx + c * 8) * 2) : kOob;
       }
-      tk = c * 8;
       td = SlotSize<NRB, WT, true>::kXOff + wave * 512;
     }
     if constexpr (NRB > 0) {
@@ -305,7 +334,6 @@ struct Feed {
       const int ci = blk * 64 + lane;
       const int r = ci / CPR, c = (ci % CPR) ^ swz_f(r);
       ao = (uint32_t)((r * p.at_sr + c * 8) * 2);
-      ak = c * 8;
       ad = BM * BK + WTile<WT>::Elems + blk * 512;
       a_on = lane >= (c0 & 63) && lane < (c0 & 63) + CPW;
     }
@@ -322,22 +350,40 @@ struct Feed {
   template <int PART>
   __device__ __forceinline__ void issue_part(const GemmArgs& p, bf16* slot, int kt) const {
     const int k0 = kt * BK;
-    if constexpr (PART == 0) {
+    const uint32_t wk0 = WT == kWNf4 || WT == kWNf4T ? (uint32_t)(k0 / 2) : (uint32_t)(k0 * wstep);
+    if (k0 + BK <= p.K) {  // the whole stage inside K: the k offset rides in the scalar offset
+      if constexpr (PART == 0) {
 #pragma unroll
-      for (int q = 0; q < XI; ++q)
-        dma16(rx, slot + xd[q], xk[q] + k0 < p.K ? xo[q] + (uint32_t)(k0 * 2) : kOob);
-      if constexpr (TALL) {
-        if (t_on) dma16(rx, slot + td, tk + k0 < p.K ? to + (uint32_t)(k0 * 2) : kOob);
+        for (int q = 0; q < XI; ++q) dma16s(rx, slot + xd[q], xo[q], (uint32_t)(k0 * 2));
+        if constexpr (TALL) {
+          if (t_on) dma16s(rx, slot + td, to, (uint32_t)(k0 * 2));
+        }
       }
-    }
-    if constexpr (PART == 1) {
+      if constexpr (PART == 1) {
 #pragma unroll
-      for (int q = 0; q < WI; ++q)
-        dma16(rw, slot + wd[q],
-              wk[q] + k0 < p.K ? wo[q] + (WT == kWNf4 || WT == kWNf4T ? (uint32_t)(k0 / 2) : (uint32_t)(k0 * wstep)) : kOob);
-    }
-    if constexpr (PART == 2 && NRB > 0) {
-      if (a_on) dma16(ra, slot + ad, ak + k0 < p.K ? ao + (uint32_t)(k0 * 2) : kOob);
+        for (int q = 0; q < WI; ++q) dma16s(rw, slot + wd[q], wo[q], wk0);
+      }
+      if constexpr (PART == 2 && NRB > 0) {
+        if (a_on) dma16s(ra, slot + ad, ao, (uint32_t)(k0 * 2));
+      }
+    } else {  // the stage crosses the end of K: each lane's k, from its lane index (kept out of the loop)
+      int lane = lane_;
+      asm volatile("" : "+v"(lane));
+      if constexpr (PART == 0) {
+#pragma unroll
+        for (int q = 0; q < XI; ++q)
+          dma16(rx, slot + xd[q], x_k(wave_, q, lane) + k0 < p.K ? xo[q] + (uint32_t)(k0 * 2) : kOob);
+        if constexpr (TALL) {
+          if (t_on) dma16(rx, slot + td, t_k(wave_, lane) + k0 < p.K ? to + (uint32_t)(k0 * 2) : kOob);
+        }
+      }
+      if constexpr (PART == 1) {
+#pragma unroll
+        for (int q = 0; q < WI; ++q) dma16(rw, slot + wd[q], w_k(wave_, q, lane) + k0 < p.K ? wo[q] + wk0 : kOob);
+      }
+      if constexpr (PART == 2 && NRB > 0) {
+        if (a_on) dma16(ra, slot + ad, a_k(wave_, lane) + k0 < p.K ? ao + (uint32_t)(k0 * 2) : kOob);
+      }
     }
     if constexpr (PART == 1 && WT == kWNf4T) {  // waves 0 .. BN/64 - 1: one row of the absmax tile each
       if (wave_ < BN / 64) {
@@ -547,28 +593,35 @@ __device__ __forceinline__ void compute(const GemmArgs& p, const bf16* slot, int
   if constexpr (AM > 0) {
 #pragma unroll
     for (int kk = 0; kk < BK / 16; ++kk) {
-      bf16x8 af[AM], bfr[FN];
-#pragma unroll
-      for (int i = 0; i < AM; ++i)
-        af[i] = *(const bf16x8*)(as + swz_rk((i * WAVES_M + wm) * 32 + (lane & 31), kk * 2 + (lane >> 5)));
-#pragma unroll
-      for (int j = 0; j < FN; ++j) {
+      auto read_a = [&](int i) -> bf16x8 {
+        return *(const bf16x8*)(as + swz_rk((i * WAVES_M + wm) * 32 + (lane & 31), kk * 2 + (lane >> 5)));
+      };
+      auto read_b = [&](int j) -> bf16x8 {
         if constexpr (WT == kWNf4T) {
           const int n = (j * WAVES_N + wn) * 32 + (lane & 31);
           const uint32_t x = *(const uint32_t*)((const uint8_t*)bs + n * (BK / 2) +
                                                 (((kk >> 1) ^ swz_q<WT>(n)) << 4) + (kk & 1) * 8 + 4 * (lane >> 5));
           const float* a = (const float*)((const uint8_t*)bs + WTile<WT>::Bytes) + (n >> 6) * BK + kk * 16 + 8 * (lane >> 5);
-          bfr[j] = nf4t_decode(x, nf.pl, *(const f32x4*)a, *(const f32x4*)(a + 4));
+          return nf4t_decode(x, nf.pl, *(const f32x4*)a, *(const f32x4*)(a + 4));
         } else if constexpr (WT == kWNf4) {
           // eight codes: byte 8kk/2 + 4(lane/32) of row n (16-byte chunk kk/2)
           const int n = (j * WAVES_N + wn) * 32 + (lane & 31);
           const uint32_t x = *(const uint32_t*)((const uint8_t*)bs + n * (BK / 2) +
                                                 (((kk >> 1) ^ swz_q<WT>(n)) << 4) + (kk & 1) * 8 + 4 * (lane >> 5));
-          bfr[j] = nf4_decode(x, tlo[j], thi[j]);
+          return nf4_decode(x, tlo[j], thi[j]);
         } else {
-          bfr[j] = w_frag<BKC, WT>(bs, (j * WAVES_N + wn) * 32, kk, lane);
+          return w_frag<BKC, WT>(bs, (j * WAVES_N + wn) * 32, kk, lane);
         }
-      }
+      };
+      // the reads in the order the MFMAs consume them (LDS returns them in order): the first MFMA
+      // waits for two fragments, each later one for at most one more
+      bf16x8 af[AM], bfr[FN];
+      bfr[0] = read_b(0);
+      af[0] = read_a(0);
+#pragma unroll
+      for (int j = 1; j < FN; ++j) bfr[j] = read_b(j);
+#pragma unroll
+      for (int i = 1; i < AM; ++i) af[i] = read_a(i);
       // the step's MFMAs at raised wave priority: of the two waves on a SIMD, the one with MFMAs ready
       // wins the issue slot over the other's LDS reads and copies (-0.85 % product time)
       __builtin_amdgcn_s_setprio(1);
