@@ -50,7 +50,8 @@ def step_flops(T, H, I, k, r):
 def gemm_launch_flops(info):
     """Algorithmic FLOP of one grouped-product launch: x W plus the LoRA x A and low B."""
     rows, K, N, r = info["rows"], info["K"], info["N"], info["rank"]
-    return 2 * rows * (K * N + K * r + r * N)
+    # an input-gradient launch that also forms B's gradient sums x^T l over its rows: K x db_rank more MACs per row
+    return 2 * rows * (K * N + K * r + r * N + K * info.get("db_rank", 0))
 
 
 # the BASELINE configurations this bench can run (1 is the headline; 2-4 are reported beside it)

@@ -155,6 +155,33 @@ int mlora_grouped_gemm_gather(const void* x, int64_t ldx, int64_t x_rows, const 
                               const void* bias, int64_t bias_se, void* out, int64_t ldo, void* low, int64_t ldl,
                               const int32_t* offsets, int E, void* stream);
 
+/* Scratch bytes mlora_grouped_gemm_db needs for (rows, K, E): fp32 partial sums, 16 x K per 256-row tile
+ * (E + rows / 256 + 1 tile slots; 16-byte aligned, contents on entry ignored). */
+size_t mlora_grouped_gemm_db_workspace_bytes(int64_t rows, int K, int E);
+
+/* The input-gradient product with the adapter gradient that reads the same rows fused into it:
+ * mlora_grouped_gemm_gather's product (gather may be NULL: rows of x read in order, x_rows = rows; a
+ * bf16 stack, adapters at rank 16, at most 256 experts), plus
+ *   db_out[e, k, r] = bf16(scaling · sum over expert e's rows of x[row, k] · l[row, r]),  k < K, r < 16,
+ * the sum mlora_grouped_reduce(_gather) forms over x's rows (g = x; with gather, row r is row
+ * gather[r] / k of x), so that the output gradient is read once, by the product.  l (rows, 16) bf16 row
+ * stride db_ldl (rows weighted as the caller needs them: mlora_grouped_reduce_gather's row_scale
+ * corresponds to l[row] = bf16(row_scale[scale_index[row]] · l[row])); db_out written by its strides
+ * (db_o_se, db_o_sk, db_o_sr).  fp32 partial sums per 256-row tile go to workspace
+ * (mlora_grouped_gemm_db_workspace_bytes) and a second launch adds each expert's tiles in row order:
+ * deterministic, no atomics.  Replaces, for the pass that reads the output gradient,
+ * _grouped_gemm_kernel's input-gradient launch and the _grouped_reduce_kernel launch for B's gradient
+ * (src/meepsquared/_grouped.py:398-399, :232-256). */
+int mlora_grouped_gemm_db(const void* x, int64_t ldx, int64_t x_rows, const int64_t* gather, int k,
+                          const void* row_scale, int row_scale_dtype, int64_t rows, int K, int N,
+                          const void* w, int64_t w_se, int64_t w_sk, int64_t w_sn, const float* scale,
+                          int scale_kind, int64_t scale_se, const void* at, int64_t at_se, int64_t at_sr,
+                          const void* bt, int64_t bt_se, int64_t bt_sn, int rank, float scaling,
+                          const void* bias, int64_t bias_se, void* out, int64_t ldo, void* low, int64_t ldl,
+                          const void* db_l, int64_t db_ldl, void* db_out, int64_t db_o_se, int64_t db_o_sk,
+                          int64_t db_o_sr, void* workspace, size_t workspace_bytes, const int32_t* offsets, int E,
+                          void* stream);
+
 /* Scratch bytes mlora_grouped_reduce(_gather) needs for (rows, N, R, E): the partial sums of split
  * experts (16-byte aligned, contents on entry ignored); 0 when no expert can be split (E > 32). */
 size_t mlora_grouped_reduce_workspace_bytes(int64_t rows, int N, int R, int E);
@@ -229,6 +256,13 @@ int mlora_combine(const void* y, int64_t H, const void* w, int w_dtype, const in
 int mlora_combine_backward(const void* dout, const void* y, int64_t H, const void* w, int w_dtype,
                            const int64_t* inv, int64_t T, int k, const int32_t* offsets, int E,
                            void* dy, void* dw, void* stream);
+
+/* out[r, :] = bf16(w[index[r]] · l[r, :]) for r < rows (l, out (rows, R) bf16, row strides ldl, ldo; R and
+ * the strides multiples of 8, 16-byte aligned bases; w bf16/f32): the down product's low weighted by each
+ * routed row's combine weight, the form mlora_grouped_gemm_db takes for B's gradient (the weighting
+ * mlora_grouped_reduce_gather's row_scale applies; src/meepsquared/_moe.py:123 weights the rows). */
+int mlora_scale_rows(const void* l, int64_t ldl, int64_t rows, int64_t R, const void* w, int w_dtype,
+                     const int64_t* index, void* out, int64_t ldo, void* stream);
 
 /* dst[e][b][a] = src[e*s_e + a*s_a + b*s_b] (bf16): a batched transpose into a contiguous (E, B, A)
  * tensor, for the adapters' roles in the input-gradient product, which

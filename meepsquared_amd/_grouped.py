@@ -408,18 +408,24 @@ class _LoraGroupedProduct(torch.autograd.Function):
                                 backward=True, products_fp8=ctx.x_fp8)
             return grad_x, None, None, None, None, None, None, None, None, None
         low = rest[0]
-        # grad_x = grad @ W (the stack read the other way) + scaling · bf16(grad @ B^T) @ A^T
-        grad_x, low2 = _launch(grad_out, weight, ctx.scale, offsets, not ctx.is_transposed, adapters.swapped(),
-                               ctx.scaling, None, True, backward=True, products_fp8=ctx.x_fp8)
+        # grad_x = grad @ W (the stack read the other way) + scaling · bf16(grad @ B^T) @ A^T, with B's
+        # gradient formed in the same pass where the kernel can (it reads grad's rows already)
+        if _db_fits(weight, adapters, offsets, ctx.x_fp8):
+            grad_x, low2, grad_b = _launch_db(grad_out, weight, ctx.scale, offsets, not ctx.is_transposed,
+                                              adapters.swapped(), ctx.scaling, low, ctx.is_transposed)
+        else:
+            grad_x, low2 = _launch(grad_out, weight, ctx.scale, offsets, not ctx.is_transposed, adapters.swapped(),
+                                   ctx.scaling, None, True, backward=True, products_fp8=ctx.x_fp8)
+            grad_b = _reduce(grad_out, low, offsets, ctx.scaling, transposed=ctx.is_transposed)
         # A's gradient (k, r) and B's (n, r), each written by the kernel in the layout of the factor it
         # belongs to, so no copy follows
         rank = adapters.rank
         if ctx.is_transposed:  # A = lhs (in, rank), B = rhs (rank, out)
             grad_lhs = _reduce(x, low2, offsets, ctx.scaling)[:, :, :rank]
-            grad_rhs = _reduce(grad_out, low, offsets, ctx.scaling, transposed=True)[:, :rank, :]
+            grad_rhs = grad_b[:, :rank, :]
         else:  # A = rhs^T, B = lhs^T
             grad_rhs = _reduce(x, low2, offsets, ctx.scaling, transposed=True)[:, :rank, :]
-            grad_lhs = _reduce(grad_out, low, offsets, ctx.scaling)[:, :, :rank]
+            grad_lhs = grad_b[:, :, :rank]
         if ctx.lhs_dtype is not None and ctx.lhs_dtype != torch.bfloat16:
             grad_lhs, grad_rhs = grad_lhs.to(ctx.lhs_dtype), grad_rhs.to(ctx.lhs_dtype)
         return grad_x, None, None, None, None, grad_lhs, grad_rhs, None, None, None
@@ -471,6 +477,73 @@ def _launch_gathered(src, perm, k, weight, scale, offsets, is_transposed, adapte
     return out, low
 
 
+def _db_fits(weight, adapters, offsets, products_fp8=False) -> bool:
+    """Whether the input-gradient product forms B's gradient itself (mlora_grouped_gemm_db): asked for with
+    MEEPSQUARED_FUSED_DB=1, and a bf16 stack tensor, adapters of rank <= 16, at most 256 experts, bf16
+    products.  Off by default: on MI355X at the Qwen3-shaped layer the fused pass costs the two input-gradient
+    launches 0.10-0.14 ms per step, about what the standalone reductions it replaces take (0.12 ms)."""
+    return (os.environ.get("MEEPSQUARED_FUSED_DB", "0") == "1" and adapters is not None and adapters.padded == 16
+            and isinstance(weight, torch.Tensor) and weight.dtype == torch.bfloat16 and not products_fp8
+            and offsets.numel() <= 256)
+
+
+def _launch_db(src, weight, scale, offsets, is_transposed, adapters, scaling, l, transposed_out, gather=None,
+               row_scale=None, db_weight=None):
+    """The input-gradient product of _launch / _launch_gathered (backward, low stored), with B's gradient
+    scaling · sum over each expert's rows of x[row]^T l'[row] formed in the same pass, x the product's input
+    rows (src, or src[perm // k] with gather=(perm, k)): the reduction _reduce(x, l, ...) would make
+    (src/meepsquared/_grouped.py:398-399), without reading x again.  row_scale: the product's output row
+    scale (as _launch_gathered's); db_weight=(w, index): l's row r weighted by w[index[r]] (rounded to bf16,
+    as _reduce weights it).  Returns (out, low, grad): grad (experts, K, 16), or (experts, 16, K) when
+    transposed_out, K = x's columns."""
+    _lib.require_gpu(src, offsets, weight, l)
+    src = src if src.stride(-1) == 1 and src.stride(0) % 8 == 0 and src.data_ptr() % 16 == 0 else src.contiguous()
+    l = l if l.stride(-1) == 1 and l.stride(0) % 8 == 0 and l.data_ptr() % 16 == 0 else l.contiguous()
+    xrows, K = src.shape
+    perm, k = gather if gather is not None else (None, 1)
+    rows = perm.numel() if gather is not None else xrows
+    E = offsets.numel()
+    N, w_se, w_sk, w_sn = _stack_strides(weight, K, is_transposed)
+    out = torch.empty((rows, N), device=src.device, dtype=torch.bfloat16)
+    R = adapters.padded
+    low = torch.empty((rows, R), device=src.device, dtype=torch.bfloat16)
+    if transposed_out:
+        grad = torch.empty((E, R, K), device=src.device, dtype=torch.bfloat16)
+        o_se, o_sk, o_sr = grad.stride(0), grad.stride(2), grad.stride(1)
+    else:
+        grad = torch.empty((E, K, R), device=src.device, dtype=torch.bfloat16)
+        o_se, o_sk, o_sr = grad.stride(0), grad.stride(1), grad.stride(2)
+    if rows == 0:
+        return out, low, grad.zero_()
+    scale_, scale_kind, scale_se, on_k = _scale_args(scale, weight, True, is_transposed)
+    if on_k:
+        raise ValueError("the fused adapter gradient takes no per-output-row stack scale in the input-gradient pass")
+    if db_weight is not None:  # l's rows weighted once, bf16(w[index[r]] · l[r]), as _reduce weights them
+        w, index = db_weight
+        w = w.reshape(-1)
+        lw = torch.empty_like(l)
+        call("mlora_scale_rows", ptr(l), l.stride(0), l.shape[0], l.shape[1], ptr(w), _lib.dtype_code(w.dtype), ptr(index),
+             ptr(lw), lw.stride(0), _lib.stream(l.device))
+        l = lw
+    ws = torch.empty(int(_lib.lib.mlora_grouped_gemm_db_workspace_bytes(rows, K, E)), device=src.device,
+                     dtype=torch.uint8)
+    info = {"rows": rows, "K": K, "N": N, "rank": adapters.rank, "db_rank": R}
+    if launch_observer is not None:
+        launch_observer("grouped_gemm", "before", info)
+    call("mlora_grouped_gemm_db", ptr(src), src.stride(0), xrows, ptr(perm), k, ptr(row_scale),
+         _lib.dtype_code(row_scale.dtype) if row_scale is not None else 0, rows, K, N,
+         ptr(weight), w_se, w_sk, w_sn, ptr(scale_), scale_kind, scale_se,
+         ptr(adapters.at), adapters.at.stride(0), adapters.at.stride(1),
+         ptr(adapters.bt), adapters.bt.stride(0), adapters.bt.stride(1),
+         R, float(scaling), None, 0, ptr(out), out.stride(0), ptr(low), low.stride(0),
+         ptr(l), l.stride(0),
+         ptr(grad), o_se, o_sk, o_sr, ptr(ws), ws.numel(),
+         ptr(offsets), E, _lib.stream(src.device))
+    if launch_observer is not None:
+        launch_observer("grouped_gemm", "after", info)
+    return out, low, grad
+
+
 class _GatheredLoraProduct(torch.autograd.Function):
     """lora_linear of x = hidden[perm // k] without materialising x: the product and A's gradient read
     the rows of hidden through perm (the fusion of src/meepsquared/_moe.py:80 into the gate_up product).
@@ -502,16 +575,21 @@ class _GatheredLoraProduct(torch.autograd.Function):
                                   backward=True)
         else:
             low = rest[0]
-            grad_sel, low2 = _launch(grad_out, weight, ctx.scale, offsets, not ctx.is_transposed, adapters.swapped(),
-                                     ctx.scaling, None, True, backward=True)
+            if _db_fits(weight, adapters, offsets):
+                grad_sel, low2, grad_b = _launch_db(grad_out, weight, ctx.scale, offsets, not ctx.is_transposed,
+                                                    adapters.swapped(), ctx.scaling, low, ctx.is_transposed)
+            else:
+                grad_sel, low2 = _launch(grad_out, weight, ctx.scale, offsets, not ctx.is_transposed,
+                                         adapters.swapped(), ctx.scaling, None, True, backward=True)
+                grad_b = _reduce(grad_out, low, offsets, ctx.scaling, transposed=ctx.is_transposed)
             rank = adapters.rank
             gather = (perm, k)
             if ctx.is_transposed:
                 grad_lhs = _reduce(hidden, low2, offsets, ctx.scaling, gather=gather)[:, :, :rank]
-                grad_rhs = _reduce(grad_out, low, offsets, ctx.scaling, transposed=True)[:, :rank, :]
+                grad_rhs = grad_b[:, :rank, :]
             else:
                 grad_rhs = _reduce(hidden, low2, offsets, ctx.scaling, transposed=True, gather=gather)[:, :rank, :]
-                grad_lhs = _reduce(grad_out, low, offsets, ctx.scaling)[:, :, :rank]
+                grad_lhs = grad_b[:, :, :rank]
             if ctx.lhs_dtype is not None and ctx.lhs_dtype != torch.bfloat16:
                 grad_lhs, grad_rhs = grad_lhs.to(ctx.lhs_dtype), grad_rhs.to(ctx.lhs_dtype)
         dh = torch.empty((T, K), device=grad_out.device, dtype=torch.bfloat16)
@@ -562,17 +640,23 @@ class _CombinedLoraProduct(torch.autograd.Function):
                                          None, row_scale=w, backward=True)
         else:
             low = rest[0]
-            grad_x, low2 = _launch_gathered(dout, perm, k, weight, ctx.scale, offsets, not ctx.is_transposed,
-                                            adapters.swapped(), ctx.scaling, None, row_scale=w, backward=True)
-            rank = adapters.rank
             ws = (w, perm)  # row r's weight: w[perm[r]]
+            if _db_fits(weight, adapters, offsets):
+                grad_x, low2, grad_b = _launch_db(dout, weight, ctx.scale, offsets, not ctx.is_transposed,
+                                                  adapters.swapped(), ctx.scaling, low, ctx.is_transposed,
+                                                  gather=(perm, k), row_scale=w, db_weight=ws)
+            else:
+                grad_x, low2 = _launch_gathered(dout, perm, k, weight, ctx.scale, offsets, not ctx.is_transposed,
+                                                adapters.swapped(), ctx.scaling, None, row_scale=w, backward=True)
+                grad_b = _reduce(dout, low, offsets, ctx.scaling, transposed=ctx.is_transposed, gather=(perm, k),
+                                 row_scale=ws)
+            rank = adapters.rank
             if ctx.is_transposed:  # A = lhs (in, rank), B = rhs (rank, out)
                 grad_lhs = _reduce(x, low2, offsets, ctx.scaling, row_scale=ws)[:, :, :rank]
-                grad_rhs = _reduce(dout, low, offsets, ctx.scaling, transposed=True, gather=(perm, k),
-                                   row_scale=ws)[:, :rank, :]
+                grad_rhs = grad_b[:, :rank, :]
             else:  # A = rhs^T, B = lhs^T
                 grad_rhs = _reduce(x, low2, offsets, ctx.scaling, transposed=True, row_scale=ws)[:, :rank, :]
-                grad_lhs = _reduce(dout, low, offsets, ctx.scaling, gather=(perm, k), row_scale=ws)[:, :, :rank]
+                grad_lhs = grad_b[:, :, :rank]
             if ctx.lhs_dtype is not None and ctx.lhs_dtype != torch.bfloat16:
                 grad_lhs, grad_rhs = grad_lhs.to(ctx.lhs_dtype), grad_rhs.to(ctx.lhs_dtype)
         dw = dw.view(ctx.wshape)
@@ -619,9 +703,14 @@ class _SwigluCombinedLoraProduct(torch.autograd.Function):
         adapters, weight, k = ctx.adapters, ctx.weight, ctx.k
         dout = dout.to(torch.bfloat16).contiguous()
         grad_lhs = grad_rhs = None
+        grad_b = None
+        ws = (w, perm)  # row r's weight: w[perm[r]]
         if adapters is None:
             g, _ = _launch_gathered(dout, perm, k, weight, ctx.scale, offsets, not ctx.is_transposed, None, 1.0, None,
                                     backward=True)
+        elif _db_fits(weight, adapters, offsets):
+            g, low2, grad_b = _launch_db(dout, weight, ctx.scale, offsets, not ctx.is_transposed, adapters.swapped(),
+                                         ctx.scaling, rest[0], ctx.is_transposed, gather=(perm, k), db_weight=ws)
         else:
             g, low2 = _launch_gathered(dout, perm, k, weight, ctx.scale, offsets, not ctx.is_transposed,
                                        adapters.swapped(), ctx.scaling, None, backward=True)
@@ -633,14 +722,15 @@ class _SwigluCombinedLoraProduct(torch.autograd.Function):
         if adapters is not None:
             low = rest[0]
             rank = adapters.rank
-            ws = (w, perm)  # row r's weight: w[perm[r]]
+            if grad_b is None:
+                grad_b = _reduce(dout, low, offsets, ctx.scaling, transposed=ctx.is_transposed, gather=(perm, k),
+                                 row_scale=ws)
             if ctx.is_transposed:  # A = lhs (in, rank), B = rhs (rank, out)
                 grad_lhs = _reduce(act, low2, offsets, ctx.scaling, row_scale=ws)[:, :, :rank]
-                grad_rhs = _reduce(dout, low, offsets, ctx.scaling, transposed=True, gather=(perm, k),
-                                   row_scale=ws)[:, :rank, :]
+                grad_rhs = grad_b[:, :rank, :]
             else:  # A = rhs^T, B = lhs^T
                 grad_rhs = _reduce(act, low2, offsets, ctx.scaling, transposed=True, row_scale=ws)[:, :rank, :]
-                grad_lhs = _reduce(dout, low, offsets, ctx.scaling, gather=(perm, k), row_scale=ws)[:, :, :rank]
+                grad_lhs = grad_b[:, :, :rank]
             if ctx.lhs_dtype is not None and ctx.lhs_dtype != torch.bfloat16:
                 grad_lhs, grad_rhs = grad_lhs.to(ctx.lhs_dtype), grad_rhs.to(ctx.lhs_dtype)
         dw = dw.view(ctx.wshape)

@@ -40,6 +40,13 @@ SIGNATURES = {
     "mlora_grouped_gemm_gather": (c_int, [P, I64, I64, P, c_int, P, c_int, I64, c_int, c_int, P, c_int, I64, I64, I64,
                                           P, c_int, I64, P, I64, I64, P, I64, I64, c_int, c_float, P, I64,
                                           P, I64, P, I64, P, c_int, P]),
+    "mlora_grouped_gemm_db_workspace_bytes": (c_size_t, [I64, c_int, c_int]),
+    "mlora_grouped_gemm_db": (c_int, [P, I64, I64, P, c_int, P, c_int, I64, c_int, c_int,
+                                      P, I64, I64, I64, P, c_int, I64,
+                                      P, I64, I64, P, I64, I64, c_int, c_float, P, I64,
+                                      P, I64, P, I64,
+                                      P, I64, P, I64, I64, I64, P, c_size_t,
+                                      P, c_int, P]),
     "mlora_grouped_reduce_workspace_bytes": (c_size_t, [I64, c_int, c_int, c_int]),
     "mlora_grouped_reduce": (c_int, [P, I64, P, I64, I64, c_int, c_int, c_float, P, c_int, P, I64, I64, I64, P, c_size_t,
                                      P]),
@@ -52,6 +59,7 @@ SIGNATURES = {
     "mlora_swiglu_backward_weighted": (c_int, [P, P, I64, I64, P, c_int, P, P, c_int, P, P, P]),
     "mlora_combine": (c_int, [P, I64, P, c_int, P, I64, c_int, P, c_int, P, P]),
     "mlora_combine_backward": (c_int, [P, P, I64, P, c_int, P, I64, c_int, P, c_int, P, P, P]),
+    "mlora_scale_rows": (c_int, [P, I64, I64, I64, P, c_int, P, P, I64, P]),
     "mlora_transpose": (c_int, [P, I64, I64, I64, I64, I64, I64, P, P]),
     "mlora_transpose_u8": (c_int, [P, I64, I64, I64, I64, I64, I64, P, P]),
     "mlora_fp8_prep": (c_int, [P, I64, I64, c_int, c_int, P, I64, P, I64, P, I64, P, I64, I64, c_int, P, I64, P, c_int,

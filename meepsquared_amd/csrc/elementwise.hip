@@ -7,6 +7,8 @@
 //   gather   src/meepsquared/_moe.py:80,85-87  selected = h[perm // k], sentinel rows zeroed
 //   SwiGLU   TF:integrations/moe.py:509-520     gate, up = chunk(2); silu(gate) * up
 //   combine  src/meepsquared/_moe.py:123-126   (out * w)[inverse].view(T, k, H).sum(1)
+//   weights  src/meepsquared/_moe.py:123         each routed row's weight, applied to the adapters' rows
+//            (l[r] weighted as the combine weights the gradient rows of the down product)
 #include <algorithm>
 
 #include "common.hpp"
@@ -378,6 +380,40 @@ extern "C" int mlora_gather_rows_backward(const void* dsel, int64_t H, const int
   }
 #undef MLORA_GRB
   return launch_status("gather_rows_backward");
+}
+
+// ---- row weights: out[r, :] = bf16(w[index[r]] · l[r, :]), one 16-byte vector per thread ----
+template <typename TW>
+__global__ __launch_bounds__(256) void scale_rows_kernel(const u32x4* __restrict__ l, int64_t ldl_v, int64_t Rv,
+                                                         const TW* __restrict__ w, const int64_t* __restrict__ index,
+                                                         int64_t rows, u32x4* __restrict__ out, int64_t ldo_v) {
+  const int64_t n = rows * Rv;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    const int64_t r = i / Rv, v = i - r * Rv;
+    const float s = load_w(w, index[r]);
+    float f[8];
+    unpack8(l[r * ldl_v + v], f);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) f[j] *= s;
+    out[r * ldo_v + v] = pack8(f);
+  }
+}
+
+extern "C" int mlora_scale_rows(const void* l, int64_t ldl, int64_t rows, int64_t R, const void* w, int w_dtype,
+                                const int64_t* index, void* out, int64_t ldo, void* stream) {
+  clear_error();
+  if (R % 8 || ldl % 8 || ldo % 8 || ldl < R || ldo < R || ((uintptr_t)l & 15u) || ((uintptr_t)out & 15u))
+    return fail("scale_rows: R (%lld) and the row strides must be multiples of 8, the bases 16-byte aligned", (long long)R);
+  if (w_dtype != MLORA_DT_BF16 && w_dtype != MLORA_DT_F32) return fail("scale_rows: w_dtype %d is not bf16/f32", w_dtype);
+  if (rows == 0) return 0;
+  const dim3 grid(grid_for(rows * (R / 8)));
+  if (w_dtype == MLORA_DT_F32)
+    hipLaunchKernelGGL(scale_rows_kernel<float>, grid, dim3(256), 0, as_stream(stream), (const u32x4*)l, ldl / 8, R / 8,
+                       (const float*)w, index, rows, (u32x4*)out, ldo / 8);
+  else
+    hipLaunchKernelGGL(scale_rows_kernel<bf16>, grid, dim3(256), 0, as_stream(stream), (const u32x4*)l, ldl / 8, R / 8,
+                       (const bf16*)w, index, rows, (u32x4*)out, ldo / 8);
+  return launch_status("scale_rows");
 }
 
 extern "C" int mlora_swiglu(const void* gu, int64_t S, int64_t I, void* act, void* stream) {

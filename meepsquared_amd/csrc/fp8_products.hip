@@ -707,7 +707,7 @@ extern "C" int mlora_fp8_gemm(const void* x8, int64_t ld8, const int32_t* xs, in
     if (bt_sn < rank || bt_sn % 8 || bt_se % 8 || !aligned16(bt)) return fail("fp8_gemm: B^T needs 16-byte aligned rows of >= rank values");
   }
   if (rows == 0) return 0;
-  f8::Args a;
+  f8::Args a{};
   GemmArgs& g = a.g;
   g.x = nullptr; g.ldx = 0; g.gather = nullptr; g.gk = 1; g.xrows = 0; g.row_scale = nullptr; g.row_scale_dt = 0;
   g.w = (const uint8_t*)w; g.w_se = w_se; g.w_sk = 1; g.w_sn = w_sn;

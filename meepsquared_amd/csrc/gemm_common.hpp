@@ -46,6 +46,14 @@ struct GemmArgs {
   const int32_t* offsets;
   int64_t rows;
   int E, K, N;
+  // The adapter gradient sum over each expert's rows of l[row] (x) x[row] (rank 16), fused into the
+  // product (bf16 stacks): NULL dbl, or rows x 16 values of l, and the fp32 workspace of per-tile
+  // partial sums, [slot][16][K].
+  const bf16* dbl;
+  int64_t dbl_ld;
+  float* dbw;
+  bf16* dbo;                 // the gradient (experts, K, 16) by its strides, written by the finishing launch
+  int64_t dbo_se, dbo_sk, dbo_sr;
 };
 
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
@@ -127,6 +135,9 @@ __device__ __forceinline__ Item decode_item(int64_t item, int nb, int E, int bm,
 
 // The bf16-stack product (grouped_gemm_bf16.hip): LDS-DMA fed, multi-stage.
 int launch_grouped_gemm_bf16(const GemmArgs& a, bool k_contiguous, hipStream_t s);
+// the fused adapter gradient's workspace rows of 16 x K fp32 (one per tile), and its expert limit
+int64_t grouped_gemm_db_slots(int64_t rows, int E);
+int grouped_gemm_db_max_experts();
 // the DMA-fed product for a quantised stack read with k contiguous (decoded in registers)
 bool grouped_gemm_dma_takes(const GemmArgs& a, int w_dtype, bool k_contiguous, bool scale_on_k);
 int launch_grouped_gemm_dma_q(const GemmArgs& a, int w_dtype, bool scale_on_k, hipStream_t s);

@@ -575,7 +575,17 @@ using namespace mlora;
 
 static bool aligned(const void* p, uintptr_t n) { return ((uintptr_t)p & (n - 1)) == 0; }
 
-static int grouped_gemm_impl(const void* x, int64_t ldx, const int64_t* gather, int gk, int64_t xrows,
+// The fused adapter gradient's arguments (mlora_grouped_gemm_db)
+struct DbIn {
+  const void* l;
+  int64_t ldl;
+  void* out;
+  int64_t o_se, o_sk, o_sr;
+  void* workspace;
+  size_t workspace_bytes;
+};
+
+static int grouped_gemm_impl(const DbIn* db, const void* x, int64_t ldx, const int64_t* gather, int gk, int64_t xrows,
                              const void* row_scale, int row_scale_dt, int64_t rows, int K, int N, const void* w,
                              int w_dtype,
                                   int64_t w_se, int64_t w_sk, int64_t w_sn, const float* scale, int scale_kind,
@@ -649,9 +659,19 @@ static int grouped_gemm_impl(const void* x, int64_t ldx, const int64_t* gather, 
     if (low != nullptr && (ldl < rank || ldl % 8 || !aligned(low, 16)))
       return fail("grouped_gemm: low needs 16-byte aligned rows of >= rank values");
   }
-  if (rows == 0) return 0;
+  if (db != nullptr) {
+    if (w_dtype != MLORA_DT_BF16) return fail("grouped_gemm_db: the fused adapter gradient takes a bf16 stack");
+    if (!lora || rank != 16) return fail("grouped_gemm_db: the fused adapter gradient needs the adapters at rank 16");
+    if (E > grouped_gemm_db_max_experts()) return fail("grouped_gemm_db: E=%d above %d", E, grouped_gemm_db_max_experts());
+    if (db->l == nullptr || db->out == nullptr) return fail("grouped_gemm_db: l and the gradient are required");
+    if (db->ldl < 16 || db->ldl % 8 || !aligned(db->l, 16)) return fail("grouped_gemm_db: l needs 16-byte aligned rows of >= 16 values");
+    const size_t need = mlora_grouped_gemm_db_workspace_bytes(rows, K, E);
+    if (db->workspace == nullptr || db->workspace_bytes < need || !aligned(db->workspace, 16))
+      return fail("grouped_gemm_db: workspace of %zu bytes, %zu needed (16-byte aligned)", db->workspace_bytes, need);
+  }
+  if (rows == 0 && db == nullptr) return 0;  // (with the fused gradient, the launch writes its zeros)
 
-  GemmArgs g;
+  GemmArgs g{};
   g.x = (const bf16*)x; g.ldx = ldx;
   g.gather = gather; g.gk = gk; g.xrows = xrows;
   g.row_scale = row_scale; g.row_scale_dt = row_scale_dt;
@@ -667,6 +687,11 @@ static int grouped_gemm_impl(const void* x, int64_t ldx, const int64_t* gather, 
   g.out = (bf16*)out; g.ldo = ldo;
   g.low = lora ? (bf16*)low : nullptr; g.ldl = ldl;
   g.offsets = offsets; g.rows = rows; g.E = E; g.K = K; g.N = N;
+  if (db != nullptr) {
+    g.dbl = (const bf16*)db->l; g.dbl_ld = db->ldl;
+    g.dbw = (float*)db->workspace;
+    g.dbo = (bf16*)db->out; g.dbo_se = db->o_se; g.dbo_sk = db->o_sk; g.dbo_sr = db->o_sr;
+  }
   hipStream_t s = as_stream(stream);
   switch (w_dtype) {
     case MLORA_DT_BF16: return launch_grouped_gemm_bf16(g, bkc, s);
@@ -691,7 +716,7 @@ extern "C" int mlora_grouped_gemm(const void* x, int64_t ldx, int64_t rows, int 
                                   const void* bt, int64_t bt_se, int64_t bt_sn, int rank, float scaling,
                                   const void* bias, int64_t bias_se, void* out, int64_t ldo, void* low, int64_t ldl,
                                   const int32_t* offsets, int E, void* stream) {
-  return grouped_gemm_impl(x, ldx, nullptr, 1, rows, nullptr, 0, rows, K, N, w, w_dtype, w_se, w_sk, w_sn, scale,
+  return grouped_gemm_impl(nullptr, x, ldx, nullptr, 1, rows, nullptr, 0, rows, K, N, w, w_dtype, w_se, w_sk, w_sn, scale,
                            scale_kind,
                            scale_se, scale_on_k, nf4_absmax_q, nf4_absmax2, nf4_code2, nf4_offset, nf4_code, at, at_se,
                            at_sr, bt, bt_se, bt_sn, rank, scaling, bias, bias_se, out, ldo, low, ldl, offsets, E, stream);
@@ -708,8 +733,37 @@ extern "C" int mlora_grouped_gemm_gather(const void* x, int64_t ldx, int64_t x_r
     clear_error();
     return fail("grouped_gemm_gather: gather is NULL");
   }
-  return grouped_gemm_impl(x, ldx, gather, k, x_rows, row_scale, row_scale_dtype, rows, K, N, w, w_dtype, w_se, w_sk,
+  return grouped_gemm_impl(nullptr, x, ldx, gather, k, x_rows, row_scale, row_scale_dtype, rows, K, N, w, w_dtype, w_se, w_sk,
                            w_sn, scale, scale_kind,
                            scale_se, 0, nullptr, nullptr, nullptr, nullptr, nullptr, at, at_se, at_sr, bt, bt_se, bt_sn,
                            rank, scaling, bias, bias_se, out, ldo, low, ldl, offsets, E, stream);
+}
+
+extern "C" size_t mlora_grouped_gemm_db_workspace_bytes(int64_t rows, int K, int E) {
+  if (rows < 0 || K < 1 || E < 1) return 0;
+  return (size_t)grouped_gemm_db_slots(rows, E) * 16 * (size_t)K * sizeof(float);
+}
+
+extern "C" int mlora_grouped_gemm_db(const void* x, int64_t ldx, int64_t x_rows, const int64_t* gather, int k,
+                                     const void* row_scale, int row_scale_dtype, int64_t rows, int K, int N,
+                                     const void* w, int64_t w_se, int64_t w_sk, int64_t w_sn, const float* scale,
+                                     int scale_kind, int64_t scale_se, const void* at, int64_t at_se, int64_t at_sr,
+                                     const void* bt, int64_t bt_se, int64_t bt_sn, int rank, float scaling,
+                                     const void* bias, int64_t bias_se, void* out, int64_t ldo, void* low, int64_t ldl,
+                                     const void* db_l, int64_t db_ldl, void* db_out, int64_t db_o_se, int64_t db_o_sk,
+                                     int64_t db_o_sr, void* workspace, size_t workspace_bytes,
+                                     const int32_t* offsets, int E, void* stream) {
+  const DbIn db{db_l, db_ldl, db_out, db_o_se, db_o_sk, db_o_sr,
+                workspace, workspace_bytes};
+  if (gather == nullptr) {
+    if (row_scale != nullptr) {
+      clear_error();
+      return fail("grouped_gemm_db: a row scale is indexed through gather");
+    }
+    x_rows = rows;
+  }
+  return grouped_gemm_impl(&db, x, ldx, gather, k, x_rows, row_scale, row_scale_dtype, rows, K, N, w, MLORA_DT_BF16,
+                           w_se, w_sk, w_sn, scale, scale_kind, scale_se, 0, nullptr, nullptr, nullptr, nullptr,
+                           nullptr, at, at_se, at_sr, bt, bt_se, bt_sn, rank, scaling, bias, bias_se, out, ldo, low,
+                           ldl, offsets, E, stream);
 }

@@ -226,9 +226,11 @@ struct SlotSize {
 // copy's scalar offset, with no per-lane test; only a stage that crosses the end of K re-derives each
 // lane's k from its lane index and sends the lanes past K out of range (zeros).  Stack columns past N
 // are read like the others (inside the stack's buffer range, or zeros past its end) and never stored.
-template <bool BKC, int NRB, int WT, bool TALL = false>
+template <bool BKC, int NRB, int WT, bool TALL = false, bool DB = false>
 struct Feed {
   static_assert(WT == kWBf16 || BKC, "fp8 and NF4 stacks are read with k contiguous");
+  static_assert(!DB || (WT == kWBf16 && NRB == 1 && STAGES == 2), "the fused adapter gradient: bf16, rank 16, two slots");
+  static constexpr bool kDB = DB;
   static constexpr int RP = NRB * 16;
   static constexpr int CPW = SlotSize<NRB, WT>::RD * BK / 8 / NW;  // A^T chunks per wave per stage
   static_assert(NRB == 0 || (CPW > 0 && 64 % CPW == 0), "each wave's A^T chunks lie in one 64-lane copy");
@@ -249,6 +251,25 @@ struct Feed {
   bool a_on;
   int lane_, wave_, n0_;
   int64_t wstep;           // bytes the stack offset advances per k (BKC: 2; else 2 * w_sk)
+  // DB: the item's share of the fused adapter gradient.  Stage kt is this item's when kt % nb == nblk
+  // (the column blocks of a row tile take turns), and on the item's j-th such stage the waves of row
+  // group j % 2 (waves 0-3 or 4-7, in turn) each sum 16 of its 64 columns over all the tile's rows.
+  const bf16* dbt_;        // LDS [BM + XR][16]: l of the tile's rows, zeros past its rows
+  rsrc_t rdbw;             // the tile's partial sums in the workspace, [16][K] fp32
+  int nb_, nblk_, mrows_;
+  mutable int db_next_, db_j_;  // the item's next such stage and how many came before it
+  // whether this wave sums on stage kt; called once per stage, in order (kt = 0, 1, ...)
+  __device__ __forceinline__ bool db_step(int kt) const {
+    if constexpr (!DB) {
+      return false;
+    } else {
+      const bool hit = kt == db_next_;
+      const bool mine = hit && (db_j_ & 1) == (wave_ >> 2);
+      db_j_ += hit ? 1 : 0;
+      db_next_ += hit ? nb_ : 0;
+      return mine;
+    }
+  }
 
   // the k (within a stage) of this lane's chunk in copy q of the x tile, the stack tile, the A^T tile
   // and the tall rows' tile
@@ -397,6 +418,56 @@ struct Feed {
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(slot + BM * BK + WTile<WT>::Bytes / 2), 4,
                                                k0 + lane_ < p.K ? (uint32_t)((k0 + lane_) * 4) : kOob, 0, 0, 0);
     }
+  }
+
+  // DB: this stage's part of the adapter gradient, columns 16 (wave % 4) .. + 15 of the stage's x tile
+  // summed over the tile's rows against l: a 16 x 16 block (column x rank) from 32-row chunks on
+  // v_mfma_f32_16x16x32_bf16, both operands read with ds_read_b64_tr_b16 (each lane gets eight rows of one
+  // column of x, or of one rank of l), then one 16-byte store per lane into the workspace ([rank][k]: lane
+  // l holds columns 4 (l / 16) .. + 3 of rank l % 16).  Every stage runs this and stores (out of range when
+  // the stage is not this wave's, the chunk loop then running no iteration): a store under a condition, in
+  // each unrolled stage, made the register allocator spill the accumulators.  The store follows the
+  // stage's copies, so the next stage's wait leaves it in flight; the prologue issues one too (db_none), so
+  // that exactly one store follows every stage's copies.
+  __device__ __forceinline__ void db_sum(const GemmArgs& p, const bf16* slot, int kt, int lane) const {
+    if constexpr (DB) {
+      typedef short s16x4 __attribute__((ext_vector_type(4)));
+      typedef short s16x8 __attribute__((ext_vector_type(8)));
+      typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+      const bool mine = db_step(kt);
+      const int nch = mine ? (mrows_ + 31) >> 5 : 0;  // at most BM / 32 + 1 (a tall item's extra rows)
+      f32x4 c0 = f32x4{}, c1 = f32x4{};
+      // two chunks per iteration into two accumulators; the addresses are formed inside the loop from the
+      // lane index taken afresh (opaque), so that stages that sum nothing spend nothing on them
+      for (int ch0 = 0; ch0 < nch; ch0 += 2) {
+        int ln = lane;
+        asm volatile("" : "+v"(ln));
+        const int G = ln >> 4, sl = ln & 15, col = (wave_ & 3) * 16 + 4 * (sl & 3);
+        bf16x8 a[2], b[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int ch = min(ch0 + u, nch - 1);  // (a chunk past nch: read, not summed)
+          const bf16* xt = ch < BM / 32 ? slot : slot + SlotSize<NRB, WT, true>::kXOff;
+          const int xr = (ch < BM / 32 ? ch * 32 : 0) + 8 * G + (sl >> 2);
+          const int lr = ch * 32 + 8 * G + (sl >> 2);
+          const s16x4 a0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(lds_void*)(xt + swz_rk(xr, col >> 3) + (col & 7)));
+          const s16x4 a1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(lds_void*)(xt + swz_rk(xr + 4, col >> 3) + (col & 7)));
+          const s16x4 b0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(lds_void*)(dbt_ + lr * 16 + 4 * (sl & 3)));
+          const s16x4 b1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(lds_void*)(dbt_ + (lr + 4) * 16 + 4 * (sl & 3)));
+          a[u] = __builtin_bit_cast(bf16x8, (s16x8{a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]}));
+          b[u] = __builtin_bit_cast(bf16x8, (s16x8{b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]}));
+        }
+        c0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0], b[0], c0, 0, 0, 0);
+        if (ch0 + 1 < nch) c1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[1], b[1], c1, 0, 0, 0);
+      }
+      c0 += c1;
+      const int k = kt * BK + (wave_ & 3) * 16 + 4 * (lane >> 4);  // K is a multiple of 8: four columns all in or all out
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, c0), rdbw,
+                                             mine && k < p.K ? (uint32_t)(((lane & 15) * p.K + k) * 4) : kOob, 0, 0);
+    }
+  }
+  __device__ __forceinline__ void db_none() const {  // the prologue's store: out of range, no effect
+    if constexpr (DB) __builtin_amdgcn_raw_buffer_store_b128(u32x4{0u, 0u, 0u, 0u}, rdbw, kOob, 0, 0);
   }
 };
 
@@ -569,11 +640,17 @@ __device__ __forceinline__ bf16x8 nf4_decode(uint32_t x, const uint32_t (&lo)[4]
 // TL: a tall item (BM + up to XR rows): one more MFMA per step into tacc, the extra rows x this wave's
 // column block wm (and their x A_e in tlacc, by waves (0, 0) and (0, 1), one 16-row half each)
 template <int AM, bool BKC, int NRB, int WT, bool TL, class F>
-__device__ __forceinline__ void compute(const GemmArgs& p, const bf16* slot, int lane, int wm, int wn,
+__device__ __forceinline__ void compute(const GemmArgs& p, const bf16* slot, int lane0, int wm, int wn,
                                         f32x16 (&acc)[FM][FN], f32x4 (&lacc)[kLS][NRB > 0 ? NRB : 1],
                                         f32x16& tacc, f32x4 (&tlacc)[NRB > 0 ? NRB : 1],
                                         Nf4Pipe& nf, const float* code, float off, int kt,
                                         const F& f, bf16* nslot, int nkt) {
+  // With the fused adapter gradient, a tall item's stages take the lane index afresh (opaque): the LDS
+  // addresses of the fragments are formed in the stage that reads them, not hoisted out of the K loop
+  // into registers held through it (the gradient's state then spills the tall accumulators).  Elsewhere
+  // the hoisted addresses are faster (4 % of the product).
+  int lane = lane0;
+  if constexpr (F::kDB && TL) asm volatile("" : "+v"(lane));
   static_assert(!TL || (AM == FM && FN == 2 && WAVES_M == 2 && WAVES_N >= 2), "tall items: 2 x 4 waves, full row blocks");
   constexpr int kXOff = SlotSize<NRB, WT, true>::kXOff;
   const bf16* as = slot;
@@ -673,6 +750,9 @@ __device__ __forceinline__ void compute(const GemmArgs& p, const bf16* slot, int
       }
     }
   }
+  if constexpr (F::kDB) {
+    f.db_sum(p, slot, kt, lane);
+  }
 }
 
 // One iteration of the K loop: wait for this wave's copies of stage kt (slot S), publish every
@@ -682,7 +762,9 @@ __device__ __forceinline__ void stage(const GemmArgs& p, const F& f, bf16* const
                                       int lane, int wm, int wn, f32x16 (&acc)[FM][FN],
                                       f32x4 (&lacc)[kLS][NRB > 0 ? NRB : 1], f32x16& tacc,
                                       f32x4 (&tlacc)[NRB > 0 ? NRB : 1], Nf4Pipe& nf, const float* code, float off) {
-  wait_vm<F::PS * (STAGES - 2)>();  // stages kt+1, kt+2 may stay in flight
+  // (stages kt+1, kt+2 may stay in flight; with the fused adapter gradient, the previous stage's store
+  // of its partial sums, issued after every copy, too)
+  wait_vm<F::PS * (STAGES - 2) + (F::kDB ? 1 : 0)>();
   stage_barrier();
   compute<AM, BKC, NRB, WT, TL>(p, slots[S], lane, wm, wn, acc, lacc, tacc, tlacc, nf, code, off, kt, f,
                                 slots[(S + STAGES - 1) % STAGES], kt + STAGES - 1);
@@ -715,7 +797,7 @@ __device__ __forceinline__ void kloop(const GemmArgs& p, const F& f, bf16* const
   }
 }
 
-template <bool BKC, int NRB, int WT, bool TALL = false>
+template <bool BKC, int NRB, int WT, bool TALL = false, bool DB = false>
 __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_kernel(GemmArgs p) {
   constexpr int RP = NRB * 16;
   constexpr int LP = RP + 8;
@@ -746,6 +828,8 @@ __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_ker
   // consecutive rows then spread over the banks.
   constexpr bool kPreB = NRB == 1;
   __shared__ __attribute__((aligned(16))) bf16 lbt[kPreB ? BN * 16 : 8];
+  // DB: l of the item's rows, [BM + XR][16] (the summed operand of the fused adapter gradient)
+  __shared__ __attribute__((aligned(16))) bf16 dbt[DB ? (BM + XR) * 16 : 8];
 
   // the small-tile counts after the tile map (experts up to kSmallLastE), then the NF4 code book (16)
   // and absmax code book (256)
@@ -787,7 +871,7 @@ __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_ker
     const int am = min(FM, max(0, (mb - wm + WAVES_M - 1) / WAVES_M));
     const int an = min(FN, max(0, (nbk - wn + WAVES_N - 1) / WAVES_N));
 
-    Feed<BKC, NRB, WT, TALL> f;
+    Feed<BKC, NRB, WT, TALL, DB> f;
     f.rx = p.gather == nullptr ? make_rsrc(p.x + row0 * p.ldx, (int64_t)mrows * p.ldx * 2)
                                : make_rsrc(p.x, p.xrows * p.ldx * 2);
     {
@@ -832,8 +916,27 @@ __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_ker
         dma16(rbt, lbt + (tid >> 6) * 512, n < p.N ? (uint32_t)((n * p.bt_sn + half * 8) * 2) : kOob);
       }
     }
+    if constexpr (DB) {
+      // l of the tile's rows into LDS by DMA, [row][16] (row r's 32 bytes are chunks 2r, 2r + 1, lane-linear:
+      // nine copies of 64 chunks); rows past the item read out of range (zeros).  They land with the first
+      // stage's copies.
+      const rsrc_t rl = make_rsrc(p.dbl + row0 * p.dbl_ld, (int64_t)mrows * p.dbl_ld * 2);
+      for (int q = wave; q < (BM + XR) * 2 / 64; q += NW) {
+        const int c = q * 64 + lane, r = c >> 1;
+        dma16(rl, dbt + q * 512, (uint32_t)((r * p.dbl_ld + (c & 1) * 8) * 2));
+      }
+      f.dbt_ = dbt;
+      f.nb_ = nb;
+      f.nblk_ = it.nblk;
+      f.db_next_ = it.nblk;
+      f.db_j_ = 0;
+      f.mrows_ = mrows;
+      // the tile's slot: expert e's tiles start at row row_start(e) + j BM, so e + row0 / BM is one per tile
+      f.rdbw = make_rsrc(p.dbw + (e + row0 / BM) * 16 * (int64_t)p.K, (int64_t)16 * p.K * 4);
+    }
 #pragma unroll
     for (int s = 0; s < STAGES - 1; ++s) f.issue(p, slots[s], s);
+    f.db_none();
 
     switch (am) {
       case FM:
@@ -1035,12 +1138,44 @@ static_assert(STAGES * SlotSize<1, kWBf16, true>::kElems * 2 + BN * 16 * 2 + kSm
 template <bool BKC, int NRB, int WT>
 constexpr bool kTallOn = STAGES == 2 && WT == kWBf16 && NRB <= 1 && WAVES_M == 2 && WAVES_N >= 2 && FN == 2;
 
-template <bool BKC, int NRB, int WT, bool TALL = false>
+// The fused adapter gradient: at most kDbMaxE experts, so that the slots, the B^T tile, l's tile and the
+// tile map fit in LDS together
+constexpr int kDbMaxE = 256;
+static_assert(STAGES * SlotSize<1, kWBf16, true>::kElems * 2 + BN * 16 * 2 + (BM + XR) * 16 * 2 + kDbMaxE * 8 <= 163840,
+              "with the fused adapter gradient: the slots, the B^T tile, l's tile and the tile map fit in LDS");
+
+// The fused adapter gradient's last step: out[e, k, r] = bf16(scaling · sum over expert e's tiles of the
+// partial sums [slot][r][k]), the tiles added in row order (deterministic).  The tiles are counted as the
+// product counts them: xr = XR when a remainder of at most XR rows joined the expert's last full tile.
+__global__ __launch_bounds__(256) void db_finish_kernel(const float* __restrict__ ws, const int32_t* __restrict__ offsets,
+                                                        int64_t rows, int E, int K, int xr, float scaling,
+                                                        bf16* __restrict__ out, int64_t o_se, int64_t o_sk,
+                                                        int64_t o_sr) {
+  const int e = blockIdx.y;
+  auto start = [&](int x) -> int64_t {
+    if (x == 0) return 0;
+    const int64_t o = offsets[x - 1];
+    return o < 0 ? 0 : (o > rows ? rows : o);
+  };
+  const int64_t es = start(e), c = start(e + 1) - es;
+  int nt = c > 0 ? (int)((c + BM - 1) / BM) : 0;
+  if (nt >= 2 && c - (int64_t)(nt - 1) * BM <= xr) --nt;
+  const int64_t s0 = e + es / BM;
+  for (int i = threadIdx.x; i < 16 * 256; i += 256) {
+    const int r = i >> 8, k = blockIdx.x * 256 + (i & 255);
+    if (k >= K) continue;
+    float sum = 0.f;
+    for (int t = 0; t < nt; ++t) sum += ws[((s0 + t) * 16 + r) * K + k];
+    out[(int64_t)e * o_se + (int64_t)k * o_sk + (int64_t)r * o_sr] = (bf16)(sum * scaling);
+  }
+}
+
+template <bool BKC, int NRB, int WT, bool TALL = false, bool DB = false>
 static int launch_t(const GemmArgs& a, hipStream_t s) {
   if constexpr (kTallOn<BKC, NRB, WT> && !TALL) {
-    if (a.E <= kSmallLastE) return launch_t<BKC, NRB, WT, true>(a, s);
+    if (a.E <= kSmallLastE) return launch_t<BKC, NRB, WT, true, DB>(a, s);
   }
-  auto kern = grouped_gemm_bf16_kernel<BKC, NRB, WT, TALL>;
+  auto kern = grouped_gemm_bf16_kernel<BKC, NRB, WT, TALL, DB>;
   const size_t lds = lds_bytes(a.E, WT);
   static std::mutex mu;
   static std::unordered_map<int64_t, int> grid_cache;
@@ -1067,6 +1202,12 @@ static int launch_t(const GemmArgs& a, hipStream_t s) {
     }
   }
   hipLaunchKernelGGL(kern, dim3(grid), dim3(kThreads), lds, s, a);
+  if constexpr (DB) {
+    if (int rc = launch_status("grouped_gemm")) return rc;
+    hipLaunchKernelGGL(db_finish_kernel, dim3((unsigned)((a.K + 255) / 256), (unsigned)a.E), dim3(256), 0, s, a.dbw,
+                       a.offsets, a.rows, a.E, a.K, TALL ? XR : 0, a.scaling, a.dbo, a.dbo_se, a.dbo_sk, a.dbo_sr);
+    return launch_status("grouped_gemm/adapter gradient");
+  }
   return launch_status("grouped_gemm");
 }
 
@@ -1085,8 +1226,16 @@ static int launch_r(const GemmArgs& a, hipStream_t s) {
 
 int launch_grouped_gemm_bf16(const GemmArgs& a, bool k_contiguous, hipStream_t s) {
   if (a.scale_kind == MLORA_SCALE_ROW && a.scale_se == 0) return fail("grouped_gemm: per-row scale without a stride");
+  if (a.dbl != nullptr) {  // with the fused adapter gradient: rank 16, at most kDbMaxE experts (checked at the ABI)
+    if (a.rank != 16 || a.E > dma::kDbMaxE) return fail("grouped_gemm: the fused adapter gradient needs rank 16 and <= %d experts", dma::kDbMaxE);
+    return k_contiguous ? dma::launch_t<true, 1, dma::kWBf16, false, true>(a, s)
+                        : dma::launch_t<false, 1, dma::kWBf16, false, true>(a, s);
+  }
   return k_contiguous ? dma::launch_r<true, dma::kWBf16>(a, s) : dma::launch_r<false, dma::kWBf16>(a, s);
 }
+
+int64_t grouped_gemm_db_slots(int64_t rows, int E) { return E + rows / dma::BM + 1; }
+int grouped_gemm_db_max_experts() { return dma::kDbMaxE; }
 
 bool grouped_gemm_dma_takes(const GemmArgs& a, int w_dtype, bool k_contiguous, bool scale_on_k) {
   // fp8 and NF4 stacks: k contiguous (each row copied as stored), rows of whole 16-byte chunks, a

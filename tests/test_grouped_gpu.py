@@ -556,3 +556,63 @@ def test_adapter_gradients_of_experts_split_into_parts(is_transposed):
         runs.append((lhs.grad.clone(), rhs.grad.clone()))
         x.grad = lhs.grad = rhs.grad = None
     assert torch.equal(runs[0][0], runs[1][0]) and torch.equal(runs[0][1], runs[1][1])
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_the_fused_adapter_gradient_matches_the_standalone_reduction(seed):
+    """mlora_grouped_gemm_db against the product launch and mlora_grouped_reduce(_gather) over the same rows:
+    the product and its low are the same bits; B's gradient (summed per 256-row tile on the MFMA, the tiles
+    added in row order) within 5e-3 of the standalone reduction and 1e-2 of an fp32 sum, and the same bits
+    on a second run.  Seeded group sizes around the tile boundaries (tall items of 513-544 rows included),
+    K a multiple of 8 but not of 64, gathered rows with per-row weights, both output layouts."""
+    from meepsquared_amd import _grouped
+
+    g = torch.Generator().manual_seed(300 + seed)
+    pick = lambda xs: xs[int(torch.randint(len(xs), (1,), generator=g))]
+    sizes = [0, 1, 31, 33, 255, 256, 257, 288, 289, 511, 513, 530, 544, 545, 700]
+    E = int(torch.randint(2, 9, (1,), generator=g))
+    rows_per_expert = [pick(sizes) for _ in range(E)]
+    K, N = 8 * int(torch.randint(4, 100, (1,), generator=g)), 8 * int(torch.randint(4, 72, (1,), generator=g))
+    is_transposed, transposed_out, gathered = bool(seed % 2), bool(seed // 2 % 2), seed >= 3
+    print("case", rows_per_expert, K, N, is_transposed, transposed_out, gathered, flush=True)
+    torch.manual_seed(seed)
+    offsets = offsets_of(rows_per_expert)
+    rows = sum(rows_per_expert)
+    weight = torch.randn((E, K, N) if is_transposed else (E, N, K), device="cuda", dtype=torch.bfloat16) * 0.05
+    lhs, rhs = adapters(E, K, N, 16, is_transposed)
+    ad = _grouped._Adapters(lhs.detach(), rhs.detach(), is_transposed)
+    l = torch.randn(rows, 16, device="cuda", dtype=torch.bfloat16)
+    if gathered:
+        k = 4
+        T = rows // k + 3
+        src = torch.randn(T, K, device="cuda", dtype=torch.bfloat16)
+        perm = torch.randperm(T * k, device="cuda")[:rows]
+        w = torch.rand(T * k, device="cuda")
+        out_r, low_r = _grouped._launch_gathered(src, perm, k, weight, None, offsets, is_transposed, ad, 2.0, None,
+                                                 row_scale=w, backward=True)
+        grad_r = _grouped._reduce(src, l, offsets, 2.0, transposed=transposed_out, gather=(perm, k), row_scale=(w, perm))
+        fused = lambda: _grouped._launch_db(src, weight, None, offsets, is_transposed, ad, 2.0, l, transposed_out,
+                                            gather=(perm, k), row_scale=w, db_weight=(w, perm))
+        x = src[perm // k].float()
+        lw = (l.float() * w[perm][:, None]).bfloat16().float()
+    else:
+        src = torch.randn(rows, K, device="cuda", dtype=torch.bfloat16)
+        out_r, low_r = _grouped._launch(src, weight, None, offsets, is_transposed, ad, 2.0, None, True, backward=True)
+        grad_r = _grouped._reduce(src, l, offsets, 2.0, transposed=transposed_out)
+        fused = lambda: _grouped._launch_db(src, weight, None, offsets, is_transposed, ad, 2.0, l, transposed_out)
+        x, lw = src.float(), l.float()
+    out, low, grad = fused()
+    assert torch.equal(out, out_r) and torch.equal(low, low_r)
+    exact = torch.zeros(E, K, 16, device="cuda")
+    starts = [0] + offsets.tolist()
+    for e in range(E):
+        a, b = starts[e], starts[e + 1]
+        exact[e] = 2.0 * (x[a:b].T @ lw[a:b])
+    if transposed_out:
+        exact = exact.transpose(1, 2)
+    assert rel(grad, grad_r) < 5e-3, rel(grad, grad_r)
+    assert rel(grad, exact) < 1e-2, rel(grad, exact)
+    for e, n in enumerate(rows_per_expert):
+        if n == 0:
+            assert torch.count_nonzero(grad[e]) == 0
+    assert torch.equal(fused()[2], grad)

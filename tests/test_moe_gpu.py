@@ -155,6 +155,21 @@ def test_layer_whose_experts_take_tall_items(is_transposed):
         assert rel(got[name], want[name]) < 1e-2, (name, rel(got[name], want[name]))
 
 
+@pytest.mark.parametrize("is_transposed", [False, True])
+def test_layer_with_the_adapter_gradient_fused_into_the_input_gradient_products(is_transposed, monkeypatch):
+    """MEEPSQUARED_FUSED_DB=1: B's gradient of both products formed by the input-gradient launches
+    (mlora_grouped_gemm_db; the down product's with the combine weights on its rows): every output and
+    gradient against the oracle, and the same as the standalone reductions give within bf16 rounding."""
+    monkeypatch.setenv("MEEPSQUARED_FUSED_DB", "1")
+    got, want = run_layer(560, 256, 192, 8, 4, 16, 32, is_transposed, seed=11)
+    for name in want:
+        assert rel(got[name], want[name]) < 1e-2, (name, rel(got[name], want[name]))
+    monkeypatch.setenv("MEEPSQUARED_FUSED_DB", "0")
+    plain, _ = run_layer(560, 256, 192, 8, 4, 16, 32, is_transposed, seed=11)
+    for name in want:
+        assert rel(got[name], plain[name]) < 5e-3, (name, rel(got[name], plain[name]))
+
+
 def test_mixtral_shaped_layer_with_zipf_loaded_experts():
     # config 2's routing (E=8, top-2, r=16, Zipf(1.2)-biased logits) at reduced width: the groups are ragged
     got, want = run_layer(1024, 512, 1792, 8, 2, 16, 32, seed=5, zipf=1.2)
