@@ -144,8 +144,9 @@ int mlora_grouped_gemm(const void* x, int64_t ldx, int64_t rows, int K, int N,
  * output row r is (c · x W + scaling · bf16(x A) B) · row_scale[gather[r]] + bias: the input gradient
  * of the down product straight from the layer's output gradient, the combine weights applied per row
  * (src/meepsquared/_moe.py:123-126 and the down projection's backward, without the weighted copy of
- * the gradient); low stays bf16(x A) of the unscaled rows.  bf16 stacks only; rows < 2^32; the other
- * arguments as mlora_grouped_gemm's (no per-row stack scale along k). */
+ * the gradient); low stays bf16(x A) of the unscaled rows.  rows < 2^32; the other arguments as
+ * mlora_grouped_gemm's (no NF4 stack and no per-row stack scale along k here: mlora_grouped_gemm_gather_q
+ * takes those); a stack layout the DMA-fed product does not take is refused. */
 int mlora_grouped_gemm_gather(const void* x, int64_t ldx, int64_t x_rows, const int64_t* gather, int k,
                               const void* row_scale, int row_scale_dtype, int64_t rows,
                               int K, int N, const void* w, int w_dtype, int64_t w_se, int64_t w_sk, int64_t w_sn,
@@ -154,6 +155,24 @@ int mlora_grouped_gemm_gather(const void* x, int64_t ldx, int64_t x_rows, const 
                               const void* bt, int64_t bt_se, int64_t bt_sn, int rank, float scaling,
                               const void* bias, int64_t bias_se, void* out, int64_t ldo, void* low, int64_t ldl,
                               const int32_t* offsets, int E, void* stream);
+
+/* mlora_grouped_gemm_gather for every stack type the DMA-fed product takes: mlora_grouped_gemm's stack
+ * arguments (w_dtype bf16, fp8 e4m3 with its scale, per-row scales along k with scale_on_k, NF4 with its
+ * tables; k contiguous for the quantised ones, rows of whole 16-byte chunks, NF4 rows of whole 64-code
+ * blocks) with the rows of x gathered and optionally weighted as mlora_grouped_gemm_gather reads them;
+ * a stack layout that product does not take is refused.  The layer's gathered gate_up product and the
+ * down product's input-gradient pass over fp8 and NF4 stacks (src/meepsquared/_moe.py:80 and :123-126
+ * folded into the products, as for bf16 stacks). */
+int mlora_grouped_gemm_gather_q(const void* x, int64_t ldx, int64_t x_rows, const int64_t* gather, int k,
+                                const void* row_scale, int row_scale_dtype, int64_t rows, int K, int N,
+                                const void* w, int w_dtype, int64_t w_se, int64_t w_sk, int64_t w_sn,
+                                const float* scale, int scale_kind, int64_t scale_se, int scale_on_k,
+                                const uint8_t* nf4_absmax_q, const float* nf4_absmax2, const float* nf4_code2,
+                                const float* nf4_offset, const float* nf4_code,
+                                const void* at, int64_t at_se, int64_t at_sr, const void* bt, int64_t bt_se,
+                                int64_t bt_sn, int rank, float scaling, const void* bias, int64_t bias_se,
+                                void* out, int64_t ldo, void* low, int64_t ldl, const int32_t* offsets, int E,
+                                void* stream);
 
 /* Scratch bytes mlora_grouped_gemm_db needs for (rows, K, E): fp32 partial sums, 16 x K per 256-row tile
  * (E + rows / 256 + 1 tile slots; 16-byte aligned, contents on entry ignored). */

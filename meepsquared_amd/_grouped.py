@@ -72,6 +72,10 @@ class Nf4Stack:
     def device(self):
         return self.packed.device
 
+    @property
+    def is_cuda(self):
+        return self.packed.is_cuda
+
     def dim(self):
         return 3
 
@@ -173,27 +177,12 @@ def _scale_args(scale, weight, backward: bool, is_transposed: bool):
                      f"({weight.shape[0]}, {out_rows}) per output row of the stack")
 
 
-def _launch(x, weight, scale, offsets, is_transposed, adapters, scaling, bias, store_low, backward=False,
-            products_fp8=False):
-    """One launch of the product kernel. Returns (out, low), low None without adapters or store_low.
-    products_fp8: the fp8 products (only for an fp8 stack; resolved by the caller as _x_fp8 does)."""
-    _lib.require_gpu(x, offsets)
-    if x.dtype != torch.bfloat16:
-        raise TypeError(f"x is {x.dtype}; the kernel computes in bf16")
-    if products_fp8:
-        return _launch_fp8(x, weight, scale, offsets, is_transposed, adapters, scaling, bias, store_low, backward)
-    rows, K = x.shape
-    if x.stride(1) != 1 or x.stride(0) % 8 or x.data_ptr() % 16:
-        x = x.contiguous()
-    N, w_se, w_sk, w_sn = _stack_strides(weight, K, is_transposed)
-    out = torch.empty((rows, N), device=x.device, dtype=x.dtype)
-    R = adapters.padded if adapters is not None else 0
-    low = torch.empty((rows, R), device=x.device, dtype=torch.bfloat16) if (adapters is not None and store_low) else None
-    if rows == 0:
-        return out, low
-    offsets = offsets if offsets.dtype == torch.int32 else offsets.to(torch.int32)
-    offsets = offsets.contiguous()
-    scale, scale_kind, scale_se, scale_on_k = _scale_args(scale, weight, backward, is_transposed)
+def _stack_operand(weight, K, N, is_transposed, scale, backward):
+    """The stack as the kernels take it: (w_ptr, w_dtype, w_se, w_sk, w_sn, the five NF4 arguments, the scale
+    arguments of _scale_args).  An NF4 stack read with n contiguous goes through its transposed codes, an fp8
+    stack read so through its k-contiguous byte copy (both made once and kept on the stack)."""
+    _, w_se, w_sk, w_sn = _stack_strides(weight, K, is_transposed)
+    scale_args = _scale_args(scale, weight, backward, is_transposed)
     nf4 = (None,) * 5
     if isinstance(weight, Nf4Stack) and w_sk != 1:
         # read with n contiguous (blocks along n): the stack's transposed codes and absmax table, kept on it
@@ -214,6 +203,31 @@ def _launch(x, weight, scale, offsets, is_transposed, adapters, scaling, bias, s
             # DMA-fed product decodes in registers
             w8, w_se, w_sn = _k_contiguous(weight, w_se, w_sk, w_sn, K, N)
             w_sk, w_ptr = 1, ptr(w8)
+    return w_ptr, w_dtype, w_se, w_sk, w_sn, nf4, scale_args
+
+
+def _launch(x, weight, scale, offsets, is_transposed, adapters, scaling, bias, store_low, backward=False,
+            products_fp8=False):
+    """One launch of the product kernel. Returns (out, low), low None without adapters or store_low.
+    products_fp8: the fp8 products (only for an fp8 stack; resolved by the caller as _x_fp8 does)."""
+    _lib.require_gpu(x, offsets)
+    if x.dtype != torch.bfloat16:
+        raise TypeError(f"x is {x.dtype}; the kernel computes in bf16")
+    if products_fp8:
+        return _launch_fp8(x, weight, scale, offsets, is_transposed, adapters, scaling, bias, store_low, backward)
+    rows, K = x.shape
+    if x.stride(1) != 1 or x.stride(0) % 8 or x.data_ptr() % 16:
+        x = x.contiguous()
+    N = _stack_strides(weight, K, is_transposed)[0]
+    out = torch.empty((rows, N), device=x.device, dtype=x.dtype)
+    R = adapters.padded if adapters is not None else 0
+    low = torch.empty((rows, R), device=x.device, dtype=torch.bfloat16) if (adapters is not None and store_low) else None
+    if rows == 0:
+        return out, low
+    offsets = offsets if offsets.dtype == torch.int32 else offsets.to(torch.int32)
+    offsets = offsets.contiguous()
+    w_ptr, w_dtype, w_se, w_sk, w_sn, nf4, (scale, scale_kind, scale_se, scale_on_k) = _stack_operand(
+        weight, K, N, is_transposed, scale, backward)
     if bias is not None:
         bias = bias.to(torch.bfloat16)
         if bias.stride(-1) != 1:
@@ -432,31 +446,43 @@ class _LoraGroupedProduct(torch.autograd.Function):
 
 
 def gathered_product_fits(weight, products_fp8=None) -> bool:
-    """Whether the product can read its rows gathered from the layer's input: a bf16 stack tensor."""
-    return isinstance(weight, torch.Tensor) and weight.dtype == torch.bfloat16 and not _x_fp8(weight, products_fp8)
+    """Whether the product can read its rows gathered from the layer's input: a bf16 or fp8 e4m3 stack tensor
+    (bf16 products) or an NF4 stack, with rows the DMA-fed product takes (16-byte chunks; NF4: 64-code blocks)."""
+    if isinstance(weight, Nf4Stack):
+        return weight.shape[1] % 64 == 0 and weight.shape[2] % 64 == 0
+    if not isinstance(weight, torch.Tensor) or _x_fp8(weight, products_fp8):
+        return False
+    if weight.dtype == torch.bfloat16:
+        return True
+    return (weight.dtype == torch.float8_e4m3fn and weight.is_contiguous() and weight.shape[1] % 16 == 0
+            and weight.shape[2] % 16 == 0 and weight.data_ptr() % 16 == 0)
 
 
 def _launch_gathered(src, perm, k, weight, scale, offsets, is_transposed, adapters, scaling, bias,
                      row_scale=None, backward=False):
-    """One launch of the product over the rows src[perm // k] (bf16 stack): (out, low).  row_scale:
-    output row r multiplied by row_scale[perm[r]] (low stays bf16 of the unscaled rows' x·A)."""
-    _lib.require_gpu(src, perm, offsets, weight)
-    if not (isinstance(weight, torch.Tensor) and weight.dtype == torch.bfloat16):
-        raise TypeError(f"the gathered product takes a bf16 stack, not {getattr(weight, 'dtype', type(weight))}: "
-                        "use lora_linear")
+    """One launch of the product over the rows src[perm // k]: (out, low).  row_scale: output row r multiplied
+    by row_scale[perm[r]] (low stays bf16 of the unscaled rows' x·A).  A bf16, fp8 (bf16 products) or NF4
+    stack, as gathered_product_fits admits."""
+    _lib.require_gpu(src, perm, offsets)
+    if not gathered_product_fits(weight, False):
+        raise TypeError(f"the gathered product takes a bf16, fp8 e4m3 or NF4 stack with rows of whole 16-byte chunks, "
+                        f"not {getattr(weight, 'dtype', type(weight))}: use lora_linear")
     src = src if src.stride(-1) == 1 and src.stride(0) % 8 == 0 and src.data_ptr() % 16 == 0 else src.contiguous()
     T, K = src.shape
     rows = perm.numel()
-    N, w_se, w_sk, w_sn = _stack_strides(weight, K, is_transposed)
+    N = _stack_strides(weight, K, is_transposed)[0]
     out = torch.empty((rows, N), device=src.device, dtype=torch.bfloat16)
     R = adapters.padded if adapters is not None else 0
     low = torch.empty((rows, R), device=src.device, dtype=torch.bfloat16) if adapters is not None else None
     if rows == 0:
         return out, low
-    scale_, scale_kind, scale_se, on_k = _scale_args(scale, weight, backward, is_transposed)
-    if on_k:  # the gathered kernel applies a per-row stack scale only along n
-        raise ValueError("the gathered product takes no per-output-row stack scale in the input-gradient pass: "
-                         "use lora_linear")
+    if (isinstance(weight, torch.Tensor) and weight.dtype == torch.bfloat16
+            and _scale_args(scale, weight, backward, is_transposed)[3]):
+        # a per-row scale along k is applied by the fp8 decode only
+        raise ValueError("the gathered product takes no per-output-row scale of a bf16 stack in the input-gradient "
+                         "pass: use lora_linear")
+    w_ptr, w_dtype, w_se, w_sk, w_sn, nf4, (scale_, scale_kind, scale_se, on_k) = _stack_operand(
+        weight, K, N, is_transposed, scale, backward)
     if bias is not None:
         bias = bias.to(torch.bfloat16)
         bias = bias if bias.stride(-1) == 1 else bias.contiguous()
@@ -464,9 +490,9 @@ def _launch_gathered(src, perm, k, weight, scale, offsets, is_transposed, adapte
     info = {"rows": rows, "K": K, "N": N, "rank": adapters.rank if adapters is not None else 0}
     if launch_observer is not None:
         launch_observer("grouped_gemm", "before", info)
-    call("mlora_grouped_gemm_gather", ptr(src), src.stride(0), T, ptr(perm), k, ptr(row_scale),
+    call("mlora_grouped_gemm_gather_q", ptr(src), src.stride(0), T, ptr(perm), k, ptr(row_scale),
          _lib.dtype_code(row_scale.dtype) if row_scale is not None else 0, rows, K, N,
-         ptr(weight), _lib.DT_BF16, w_se, w_sk, w_sn, ptr(scale_), scale_kind, scale_se,
+         w_ptr, w_dtype, w_se, w_sk, w_sn, ptr(scale_), scale_kind, scale_se, on_k, *nf4,
          ptr(at), at.stride(0) if at is not None else 0, at.stride(1) if at is not None else 0,
          ptr(bt), bt.stride(0) if bt is not None else 0, bt.stride(1) if bt is not None else 0,
          R, float(scaling), ptr(bias), bias.stride(0) if bias is not None else 0,
@@ -741,14 +767,15 @@ class _SwigluCombinedLoraProduct(torch.autograd.Function):
 
 def swiglu_lora_linear_combined(gu, weights, perm, inv, k, weight, scale, offsets, is_transposed, lhs=None, rhs=None,
                                 scaling: float = 1.0):
-    """combine(lora_linear(swiglu(gu), ...), weights) of the layer's down product (bf16 stack, no bias)."""
+    """combine(lora_linear(swiglu(gu), ...), weights) of the layer's down product (a stack gathered_product_fits
+    admits, no bias)."""
     return _SwigluCombinedLoraProduct.apply(gu, weights, perm, inv, k, weight, scale, offsets, is_transposed, lhs,
                                             rhs, scaling)
 
 
 def lora_linear_combined(x, weights, perm, inv, k, weight, scale, offsets, is_transposed, lhs=None, rhs=None,
                          scaling: float = 1.0, bias=None):
-    """combine(lora_linear(x, ...), weights) of the layer's down product (bf16 stacks), its backward
+    """combine(lora_linear(x, ...), weights) of the layer's down product (stacks gathered_product_fits admits), its backward
     reading the output gradient through perm instead of a weighted copy of it."""
     return _CombinedLoraProduct.apply(x, weights, perm, inv, k, weight, scale, offsets, is_transposed, lhs, rhs,
                                       scaling, bias)
@@ -756,7 +783,8 @@ def lora_linear_combined(x, weights, perm, inv, k, weight, scale, offsets, is_tr
 
 def lora_linear_gathered(hidden, perm, inv, k, weight, scale, offsets, is_transposed, lhs=None, rhs=None,
                          scaling: float = 1.0, bias=None):
-    """lora_linear(hidden[perm // k], ...) with the gathered rows never materialised (bf16 stacks)."""
+    """lora_linear(hidden[perm // k], ...) with the gathered rows never materialised (bf16, fp8 or NF4 stacks,
+    as gathered_product_fits admits)."""
     return _GatheredLoraProduct.apply(hidden, perm, inv, k, weight, scale, offsets, is_transposed, lhs, rhs, scaling,
                                       bias)
 

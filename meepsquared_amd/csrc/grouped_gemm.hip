@@ -598,7 +598,6 @@ static int grouped_gemm_impl(const DbIn* db, const void* x, int64_t ldx, const i
   clear_error();
   if (rows < 0) return fail("grouped_gemm: rows=%lld is negative", (long long)rows);
   if (gather != nullptr) {
-    if (w_dtype != MLORA_DT_BF16) return fail("grouped_gemm_gather: gathered rows need a bf16 stack");
     if (gk < 1) return fail("grouped_gemm_gather: k=%d must be >= 1", gk);
     if (rows > (int64_t)0xFFFFFFFFu) return fail("grouped_gemm_gather: rows=%lld must be below 2^32", (long long)rows);
     if (xrows < 0 || xrows * ldx * 2 > 0x7FFFFFF0) return fail("grouped_gemm_gather: x (%lld rows) exceeds 2 GiB", (long long)xrows);
@@ -693,10 +692,14 @@ static int grouped_gemm_impl(const DbIn* db, const void* x, int64_t ldx, const i
     g.dbo = (bf16*)db->out; g.dbo_se = db->o_se; g.dbo_sk = db->o_sk; g.dbo_sr = db->o_sr;
   }
   hipStream_t s = as_stream(stream);
+  // gathered rows are read by the DMA-fed product only (every stack type it takes)
+  const char* no_gather = "grouped_gemm_gather: gathered rows need a stack the DMA-fed product takes (k contiguous, "
+                          "16-byte aligned rows; NF4: rows of whole 64-code blocks)";
   switch (w_dtype) {
     case MLORA_DT_BF16: return launch_grouped_gemm_bf16(g, bkc, s);
     case MLORA_DT_FP8_E4M3:
       if (grouped_gemm_dma_takes(g, w_dtype, bkc, scale_k)) return launch_grouped_gemm_dma_q(g, w_dtype, scale_k, s);
+      if (gather != nullptr) return fail("%s", no_gather);
       if (scale_k) return bkc ? launch_r<W_FP8, true, true>(g, s) : launch_r<W_FP8, false, true>(g, s);
       return bkc ? launch_r<W_FP8, true, false>(g, s) : launch_r<W_FP8, false, false>(g, s);
     case MLORA_DT_NF4_KT:
@@ -704,6 +707,7 @@ static int grouped_gemm_impl(const DbIn* db, const void* x, int64_t ldx, const i
       return fail("grouped_gemm: NF4 codes along k need a 16-byte aligned stack");
     default:
       if (grouped_gemm_dma_takes(g, w_dtype, bkc, false)) return launch_grouped_gemm_dma_q(g, w_dtype, false, s);
+      if (gather != nullptr) return fail("%s", no_gather);
       return bkc ? launch_r<W_NF4, true, false>(g, s) : launch_r<W_NF4, false, false>(g, s);
   }
 }
@@ -737,6 +741,26 @@ extern "C" int mlora_grouped_gemm_gather(const void* x, int64_t ldx, int64_t x_r
                            w_sn, scale, scale_kind,
                            scale_se, 0, nullptr, nullptr, nullptr, nullptr, nullptr, at, at_se, at_sr, bt, bt_se, bt_sn,
                            rank, scaling, bias, bias_se, out, ldo, low, ldl, offsets, E, stream);
+}
+
+extern "C" int mlora_grouped_gemm_gather_q(const void* x, int64_t ldx, int64_t x_rows, const int64_t* gather, int k,
+                                           const void* row_scale, int row_scale_dtype, int64_t rows, int K, int N,
+                                           const void* w, int w_dtype, int64_t w_se, int64_t w_sk, int64_t w_sn,
+                                           const float* scale, int scale_kind, int64_t scale_se, int scale_on_k,
+                                           const uint8_t* nf4_absmax_q, const float* nf4_absmax2,
+                                           const float* nf4_code2, const float* nf4_offset, const float* nf4_code,
+                                           const void* at, int64_t at_se, int64_t at_sr, const void* bt, int64_t bt_se,
+                                           int64_t bt_sn, int rank, float scaling, const void* bias, int64_t bias_se,
+                                           void* out, int64_t ldo, void* low, int64_t ldl, const int32_t* offsets, int E,
+                                           void* stream) {
+  if (gather == nullptr) {
+    clear_error();
+    return fail("grouped_gemm_gather_q: gather is NULL");
+  }
+  return grouped_gemm_impl(nullptr, x, ldx, gather, k, x_rows, row_scale, row_scale_dtype, rows, K, N, w, w_dtype,
+                           w_se, w_sk, w_sn, scale, scale_kind, scale_se, scale_on_k, nf4_absmax_q, nf4_absmax2,
+                           nf4_code2, nf4_offset, nf4_code, at, at_se, at_sr, bt, bt_se, bt_sn, rank, scaling, bias,
+                           bias_se, out, ldo, low, ldl, offsets, E, stream);
 }
 
 extern "C" size_t mlora_grouped_gemm_db_workspace_bytes(int64_t rows, int K, int E) {

@@ -366,35 +366,43 @@ def test_the_fp8_activation_pass_is_bit_exact(K, colscale, terms):
     assert rel(low.float().cpu(), low_ref) < 1e-2
 
 
+@pytest.mark.parametrize("kind", ["bf16", "fp8", "nf4"])
 @pytest.mark.parametrize("is_transposed", [False, True])
 @pytest.mark.parametrize("T", [300, 600])  # 600 tokens: ~300 rows per expert, tall items among them
-def test_the_gathered_product_is_bit_identical_to_the_product_of_the_gathered_rows(is_transposed, T):
+def test_the_gathered_product_is_bit_identical_to_the_product_of_the_gathered_rows(is_transposed, T, kind):
     """lora_linear_gathered (rows read through perm, never materialised) against lora_linear on
-    hidden[perm // k]: the same tiles and the same sums, so the same bits, gradients included."""
-    from meepsquared_amd import _grouped, lora_linear, sort_by_expert
+    hidden[perm // k]: the same tiles and the same sums, so the same bits, gradients included; for bf16,
+    fp8 (one scale per output row) and NF4 stacks."""
+    from meepsquared_amd import _fp8, _grouped, _nf4, lora_linear, sort_by_expert
     from meepsquared_amd._moe import _Gather
 
     torch.manual_seed(5)
-    k, E, K, N, r = 3, 6, 192, 160, 16
+    k, E, K, N, r = 3, 6, 192, 128, 16
     idx = torch.randint(0, E, (T, k), device="cuda")
     idx[::11, 0] = E  # sentinel ids: rows after every expert
     perm, inv, offsets = sort_by_expert(idx, E)
     h = torch.randn(T, K, device="cuda", dtype=torch.bfloat16)
     weight = torch.randn((E, K, N) if is_transposed else (E, N, K), device="cuda", dtype=torch.bfloat16) * 0.05
+    scale = None
+    if kind == "fp8":
+        weight, scale = _fp8.quantize_stack(weight, per_row=True, is_transposed=is_transposed)
+    elif kind == "nf4":
+        weight = _nf4.quantize_stack(weight)
+    assert _grouped.gathered_product_fits(weight, False)
     lhs, rhs = adapters(E, K, N, r, is_transposed)
     bias = torch.randn(E, N, device="cuda", dtype=torch.bfloat16)
     grad = torch.randn(T * k, N, device="cuda", dtype=torch.bfloat16)
     live = int(offsets[-1])
 
     h1 = h.clone().requires_grad_()
-    out1 = _grouped.lora_linear_gathered(h1, perm, inv, k, weight, None, offsets, is_transposed, lhs, rhs, 2.0, bias)
+    out1 = _grouped.lora_linear_gathered(h1, perm, inv, k, weight, scale, offsets, is_transposed, lhs, rhs, 2.0, bias)
     out1[:live].backward(grad[:live])
     g1 = (out1[:live].detach().clone(), h1.grad.clone(), lhs.grad.clone(), rhs.grad.clone())
     lhs.grad = rhs.grad = None
 
     h2 = h.clone().requires_grad_()
     sel = _Gather.apply(h2, perm, inv, offsets, k)  # the materialised rows, through the same gather kernel
-    out2 = lora_linear(sel, weight, None, offsets, is_transposed, lhs, rhs, 2.0, bias)
+    out2 = lora_linear(sel, weight, scale, offsets, is_transposed, lhs, rhs, 2.0, bias, products_fp8=False)
     out2[:live].backward(grad[:live])
     g2 = (out2[:live].detach(), h2.grad, lhs.grad, rhs.grad)
     for name, a, b in zip(("out", "grad_h", "grad_lhs", "grad_rhs"), g1, g2):
@@ -511,17 +519,23 @@ def test_a_scale_of_the_wrong_shape_is_refused(is_transposed):
 
 
 def test_the_gathered_products_refuse_what_their_kernel_does_not_take():
-    """The gathered product reads bf16 stacks only and applies no per-row stack scale along k: an fp8
-    stack is a TypeError, a per-row scale in the input-gradient pass a ValueError (lora_linear takes both)."""
+    """The gathered product reads bf16, fp8 and NF4 stacks whose rows are whole 16-byte chunks (NF4: 64-code
+    blocks) and applies a per-row stack scale along k only in the fp8 decode: an fp8 stack with rows of 72
+    bytes and a float32 stack are TypeErrors, a bf16 stack's per-row scale in the input-gradient pass a
+    ValueError (lora_linear takes all three)."""
     from meepsquared_amd import _fp8, _grouped, sort_by_expert
 
-    E, K, N, k, T = 3, 64, 48, 2, 20
+    E, K, N, k, T = 3, 72, 48, 2, 20
     idx = torch.randint(0, E, (T, k), device="cuda")
     perm, inv, offsets = sort_by_expert(idx, E)
     h = torch.randn(T, K, device="cuda", dtype=torch.bfloat16)
     w8, s8 = _fp8.quantize_stack(torch.randn(E, N, K, device="cuda") * 0.05, per_row=True)
-    with pytest.raises(TypeError, match="bf16 stack"):
+    with pytest.raises(TypeError, match="16-byte chunks"):
         _grouped.lora_linear_gathered(h, perm, inv, k, w8, s8, offsets, False)
+    with pytest.raises(TypeError, match="16-byte chunks"):
+        _grouped.lora_linear_gathered(h, perm, inv, k, torch.randn(E, N, K, device="cuda"), None, offsets, False)
+    K = 64
+    h = torch.randn(T, K, device="cuda", dtype=torch.bfloat16)
     wb = torch.randn(E, N, K, device="cuda", dtype=torch.bfloat16)
     x = torch.randn(T * k, K, device="cuda", dtype=torch.bfloat16, requires_grad=True)
     wts = torch.rand(T, k, device="cuda")
