@@ -164,7 +164,7 @@ def roofline(c, achieved, config):
                                            "step, timed together)",
                 "achieved": round(achieved, 2), "peak": PEAK_FP8_TFLOPS, "unit": "TFLOP/s",
                 "frac": round(achieved / PEAK_FP8_TFLOPS, 4), "traffic": None}
-    kernel = ("grouped_gemm_kernel (register-staged, NF4 decoded in registers; 4 launches per step)"
+    kernel = ("grouped_gemm_bf16_kernel (DMA-fed, NF4 stacks decoded in registers; 4 launches per step)"
               if c.get("stack") == "nf4" else
               "grouped_gemm_bf16_kernel (4 launches per step; traffic = mean HBM bytes per launch, rocprofv3 PMC)")
     return {"bound": "mfma", "kernel": kernel, "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
