@@ -263,6 +263,30 @@ int mlora_swiglu_backward_weighted(const void* gu, const void* g, int64_t S, int
                                    const int64_t* perm, const int32_t* offsets, int E, void* dgu, void* dw,
                                    void* stream);
 
+/* mlora_swiglu_backward_weighted fused with the two adapter reductions that read its operands (no
+ * counterpart function in the reference: it replaces, in one pass over each expert's rows, the SwiGLU
+ * gate's backward and the weighted combine's (src/meepsquared/_moe.py:118-126) and two of the
+ * _reduce calls of src/meepsquared/_grouped.py:362-370, 398-399):
+ *   dgu, dw             as mlora_swiglu_backward_weighted (dgu bit-identical; dw summed per 64 columns,
+ *                       then over the column blocks in order);
+ *   dA[e, n, r]         = bf16(scaling2 · sum over expert e's rows p of act[p, n] · bf16(w[perm[p]] · low2[p, r]))
+ *                         (the down adapter's A gradient: act as mlora_swiglu rounds it, low2 (S, 16) the
+ *                         down input-gradient product's low, unweighted, row stride ld2);
+ *   dB[e, n, r]         = bf16(scaling_gu · sum over expert e's rows p of dgu[p, n] · lowgu[p, r]) for n < 2I
+ *                         (the gate_up adapter's B gradient: lowgu (S, 16) the gate_up product's low);
+ * each the same bits as mlora_grouped_reduce_gather(act, low2, row_scale w) and mlora_grouped_reduce(dgu,
+ * lowgu) give.  dA and dB are written by their strides (se, sn, sr).  Rank 16 (padded) only; I % 8 == 0;
+ * bf16 tensors 16-byte aligned.  The workspace (256-byte aligned) holds per-row parts of dw and, when an
+ * expert's rows can be split over several workgroups, their partial sums:
+ * mlora_swiglu_backward_reduce_workspace_bytes gives its size. */
+size_t mlora_swiglu_backward_reduce_workspace_bytes(int64_t S, int64_t I, int E);
+int mlora_swiglu_backward_reduce(const void* gu, const void* g, int64_t S, int64_t I, const void* w, int w_dtype,
+                                 const int64_t* perm, const int32_t* offsets, int E, const void* low2, int64_t ld2,
+                                 float scaling2, void* dA, int64_t a_se, int64_t a_sn, int64_t a_sr,
+                                 const void* lowgu, int64_t ldu, float scaling_gu, void* dB, int64_t b_se,
+                                 int64_t b_sn, int64_t b_sr, void* dgu, void* dw, void* workspace,
+                                 size_t workspace_bytes, void* stream);
+
 /* out[t, :] = sum over j < k of bf16(y[inv[t*k+j], :] · w[t*k+j]) with fp32 accumulation; rows at
  * or past offsets[E-1] (sentinels) contribute nothing.  y (S, H) contiguous, w (T*k) of w_dtype
  * (MLORA_DT_BF16 or MLORA_DT_F32), out (T, H) contiguous.  Replaces _moe.py:123-126. */

@@ -355,6 +355,15 @@ def _launch_fp8(x, weight, scale, offsets, is_transposed, adapters, scaling, bia
     return out, (low if store_low else None)
 
 
+def _reduce_out(experts: int, N: int, R: int, transposed: bool, device):
+    """The (experts, N, R) bf16 gradient, or (experts, R, N) when transposed, and its (se, sn, sr) strides."""
+    if transposed:
+        out = torch.empty((experts, R, N), device=device, dtype=torch.bfloat16)
+        return out, (out.stride(0), out.stride(2), out.stride(1))
+    out = torch.empty((experts, N, R), device=device, dtype=torch.bfloat16)
+    return out, (out.stride(0), out.stride(1), out.stride(2))
+
+
 def _reduce(g: torch.Tensor, low: torch.Tensor, offsets: torch.Tensor, scaling: float,
             transposed: bool = False, gather=None, row_scale=None) -> torch.Tensor:
     """(experts, N, R) bf16: scaling · sum over each expert's rows of g^T @ low (_grouped.py:362-370);
@@ -570,13 +579,34 @@ def _launch_db(src, weight, scale, offsets, is_transposed, adapters, scaling, l,
     return out, low, grad
 
 
+class GateUpLink:
+    """What the layer's two Functions share so that the SwiGLU backward also forms the gate_up adapter's B
+    gradient (mlora_swiglu_backward_reduce): the gate_up product's forward leaves its low rows and scaling
+    here, the down Function's backward leaves that gradient and the dgu it was formed from, and the gate_up
+    backward takes it when its incoming gradient is that very dgu (else it reduces as usual)."""
+
+    __slots__ = ("low", "scaling", "transposed", "padded", "grad_b", "dgu", "dgu_version")
+
+    def __init__(self):
+        self.low = self.grad_b = self.dgu = None
+        self.scaling, self.transposed, self.padded, self.dgu_version = 1.0, False, 0, -1
+
+    def take(self, grad_out):
+        """The B gradient formed for grad_out, or None."""
+        grad_b, dgu = self.grad_b, self.dgu
+        self.grad_b = self.dgu = None
+        if grad_b is None or grad_out is not dgu or grad_out._version != self.dgu_version:
+            return None
+        return grad_b
+
+
 class _GatheredLoraProduct(torch.autograd.Function):
     """lora_linear of x = hidden[perm // k] without materialising x: the product and A's gradient read
     the rows of hidden through perm (the fusion of src/meepsquared/_moe.py:80 into the gate_up product).
     Gradients for hidden (each token's k rows summed) and the adapters."""
 
     @staticmethod
-    def forward(ctx, hidden, perm, inv, k, weight, scale, offsets, is_transposed, lhs, rhs, scaling, bias):
+    def forward(ctx, hidden, perm, inv, k, weight, scale, offsets, is_transposed, lhs, rhs, scaling, bias, link=None):
         _lib.require_gpu(hidden, perm, offsets, weight)
         hidden = hidden if hidden.stride(-1) == 1 and hidden.stride(0) % 8 == 0 and hidden.data_ptr() % 16 == 0 \
             else hidden.contiguous()
@@ -584,6 +614,9 @@ class _GatheredLoraProduct(torch.autograd.Function):
         adapters = _Adapters(lhs, rhs, is_transposed) if lhs is not None else None
         out, low = _launch_gathered(hidden, perm, k, weight, scale, offsets, is_transposed, adapters, scaling, bias)
         ctx.save_for_backward(hidden, perm, inv, offsets, *((low,) if low is not None else ()))
+        ctx.link = link
+        if link is not None and adapters is not None:
+            link.low, link.scaling, link.transposed, link.padded = low, scaling, is_transposed, adapters.padded
         ctx.weight, ctx.adapters, ctx.scale = weight, adapters, scale
         ctx.is_transposed, ctx.scaling, ctx.k = is_transposed, scaling, k
         ctx.lhs_dtype = lhs.dtype if lhs is not None else None
@@ -601,13 +634,15 @@ class _GatheredLoraProduct(torch.autograd.Function):
                                   backward=True)
         else:
             low = rest[0]
-            if _db_fits(weight, adapters, offsets):
+            grad_b = ctx.link.take(grad_out) if ctx.link is not None else None  # formed by the SwiGLU backward
+            if grad_b is None and _db_fits(weight, adapters, offsets):
                 grad_sel, low2, grad_b = _launch_db(grad_out, weight, ctx.scale, offsets, not ctx.is_transposed,
                                                     adapters.swapped(), ctx.scaling, low, ctx.is_transposed)
             else:
                 grad_sel, low2 = _launch(grad_out, weight, ctx.scale, offsets, not ctx.is_transposed,
                                          adapters.swapped(), ctx.scaling, None, True, backward=True)
-                grad_b = _reduce(grad_out, low, offsets, ctx.scaling, transposed=ctx.is_transposed)
+                if grad_b is None:
+                    grad_b = _reduce(grad_out, low, offsets, ctx.scaling, transposed=ctx.is_transposed)
             rank = adapters.rank
             gather = (perm, k)
             if ctx.is_transposed:
@@ -621,7 +656,7 @@ class _GatheredLoraProduct(torch.autograd.Function):
         dh = torch.empty((T, K), device=grad_out.device, dtype=torch.bfloat16)
         call("mlora_gather_rows_backward", ptr(grad_sel), K, ptr(inv), T, k, ptr(offsets), offsets.numel(),
              ptr(dh), _lib.stream(grad_out.device))
-        return dh, None, None, None, None, None, None, None, grad_lhs, grad_rhs, None, None
+        return dh, None, None, None, None, None, None, None, grad_lhs, grad_rhs, None, None, None
 
 
 class _CombinedLoraProduct(torch.autograd.Function):
@@ -700,7 +735,7 @@ class _SwigluCombinedLoraProduct(torch.autograd.Function):
     the weights and the adapters."""
 
     @staticmethod
-    def forward(ctx, gu, weights, perm, inv, k, weight, scale, offsets, is_transposed, lhs, rhs, scaling):
+    def forward(ctx, gu, weights, perm, inv, k, weight, scale, offsets, is_transposed, lhs, rhs, scaling, link=None):
         offsets = offsets.to(torch.int32).contiguous()
         gu = gu.contiguous()
         S, I2 = gu.shape
@@ -721,6 +756,7 @@ class _SwigluCombinedLoraProduct(torch.autograd.Function):
         ctx.is_transposed, ctx.scaling, ctx.k = is_transposed, scaling, k
         ctx.lhs_dtype = lhs.dtype if lhs is not None else None
         ctx.wshape, ctx.wdtype = weights.shape, weights.dtype
+        ctx.link = link
         return out
 
     @staticmethod
@@ -743,34 +779,55 @@ class _SwigluCombinedLoraProduct(torch.autograd.Function):
         S, I = g.shape
         dgu = torch.empty_like(gu)
         dw = torch.empty_like(w)
-        call("mlora_swiglu_backward_weighted", ptr(gu), ptr(g), S, I, ptr(w), _lib.dtype_code(w.dtype), ptr(perm),
-             ptr(offsets), offsets.numel(), ptr(dgu), ptr(dw), _lib.stream(gu.device))
+        link = ctx.link
+        grad_a = None  # A's gradient of the down adapter, (E, I, R) or (E, R, I) as _reduce lays it out
+        if (adapters is not None and adapters.padded == 16 and link is not None and link.low is not None
+                and link.padded == 16 and S > 0):
+            # the SwiGLU backward with A's gradient of the down adapter and B's of the gate_up adapter
+            E = offsets.numel()
+            low2_ = low2 if low2.stride(1) == 1 else low2.contiguous()
+            lowgu = link.low
+            grad_a, a_strides = _reduce_out(E, I, 16, not ctx.is_transposed, gu.device)
+            grad_bgu, b_strides = _reduce_out(E, 2 * I, 16, link.transposed, gu.device)
+            ws_ = torch.empty(int(_lib.lib.mlora_swiglu_backward_reduce_workspace_bytes(S, I, E)), device=gu.device,
+                              dtype=torch.uint8)
+            call("mlora_swiglu_backward_reduce", ptr(gu), ptr(g), S, I, ptr(w), _lib.dtype_code(w.dtype), ptr(perm),
+                 ptr(offsets), E, ptr(low2_), low2_.stride(0), float(ctx.scaling), ptr(grad_a), *a_strides,
+                 ptr(lowgu), lowgu.stride(0), float(link.scaling), ptr(grad_bgu), *b_strides, ptr(dgu), ptr(dw),
+                 ptr(ws_), ws_.numel(), _lib.stream(gu.device))
+            link.grad_b, link.dgu, link.dgu_version = grad_bgu, dgu, dgu._version
+        else:
+            call("mlora_swiglu_backward_weighted", ptr(gu), ptr(g), S, I, ptr(w), _lib.dtype_code(w.dtype),
+                 ptr(perm), ptr(offsets), offsets.numel(), ptr(dgu), ptr(dw), _lib.stream(gu.device))
         if adapters is not None:
             low = rest[0]
             rank = adapters.rank
             if grad_b is None:
                 grad_b = _reduce(dout, low, offsets, ctx.scaling, transposed=ctx.is_transposed, gather=(perm, k),
                                  row_scale=ws)
+            if grad_a is None:
+                grad_a = _reduce(act, low2, offsets, ctx.scaling, transposed=not ctx.is_transposed, row_scale=ws)
             if ctx.is_transposed:  # A = lhs (in, rank), B = rhs (rank, out)
-                grad_lhs = _reduce(act, low2, offsets, ctx.scaling, row_scale=ws)[:, :, :rank]
+                grad_lhs = grad_a[:, :, :rank]
                 grad_rhs = grad_b[:, :rank, :]
             else:  # A = rhs^T, B = lhs^T
-                grad_rhs = _reduce(act, low2, offsets, ctx.scaling, transposed=True, row_scale=ws)[:, :rank, :]
+                grad_rhs = grad_a[:, :rank, :]
                 grad_lhs = grad_b[:, :, :rank]
             if ctx.lhs_dtype is not None and ctx.lhs_dtype != torch.bfloat16:
                 grad_lhs, grad_rhs = grad_lhs.to(ctx.lhs_dtype), grad_rhs.to(ctx.lhs_dtype)
         dw = dw.view(ctx.wshape)
         if dw.dtype != ctx.wdtype:
             dw = dw.to(ctx.wdtype)
-        return dgu, dw, None, None, None, None, None, None, None, grad_lhs, grad_rhs, None
+        return dgu, dw, None, None, None, None, None, None, None, grad_lhs, grad_rhs, None, None
 
 
 def swiglu_lora_linear_combined(gu, weights, perm, inv, k, weight, scale, offsets, is_transposed, lhs=None, rhs=None,
-                                scaling: float = 1.0):
+                                scaling: float = 1.0, link: GateUpLink = None):
     """combine(lora_linear(swiglu(gu), ...), weights) of the layer's down product (a stack gathered_product_fits
-    admits, no bias)."""
+    admits, no bias).  link: shared with the lora_linear_gathered call that produced gu, so that the SwiGLU
+    backward forms that product's B gradient too."""
     return _SwigluCombinedLoraProduct.apply(gu, weights, perm, inv, k, weight, scale, offsets, is_transposed, lhs,
-                                            rhs, scaling)
+                                            rhs, scaling, link)
 
 
 def lora_linear_combined(x, weights, perm, inv, k, weight, scale, offsets, is_transposed, lhs=None, rhs=None,
@@ -782,11 +839,11 @@ def lora_linear_combined(x, weights, perm, inv, k, weight, scale, offsets, is_tr
 
 
 def lora_linear_gathered(hidden, perm, inv, k, weight, scale, offsets, is_transposed, lhs=None, rhs=None,
-                         scaling: float = 1.0, bias=None):
+                         scaling: float = 1.0, bias=None, link: GateUpLink = None):
     """lora_linear(hidden[perm // k], ...) with the gathered rows never materialised (bf16, fp8 or NF4 stacks,
-    as gathered_product_fits admits)."""
+    as gathered_product_fits admits).  link: see swiglu_lora_linear_combined."""
     return _GatheredLoraProduct.apply(hidden, perm, inv, k, weight, scale, offsets, is_transposed, lhs, rhs, scaling,
-                                      bias)
+                                      bias, link)
 
 
 def lora_linear(x, weight, scale, offsets, is_transposed: bool, lhs=None, rhs=None, scaling: float = 1.0, bias=None,

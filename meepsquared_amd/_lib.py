@@ -62,6 +62,9 @@ SIGNATURES = {
     "mlora_swiglu": (c_int, [P, I64, I64, P, P]),
     "mlora_swiglu_backward": (c_int, [P, P, I64, I64, P, P]),
     "mlora_swiglu_backward_weighted": (c_int, [P, P, I64, I64, P, c_int, P, P, c_int, P, P, P]),
+    "mlora_swiglu_backward_reduce_workspace_bytes": (c_size_t, [I64, I64, c_int]),
+    "mlora_swiglu_backward_reduce": (c_int, [P, P, I64, I64, P, c_int, P, P, c_int, P, I64, c_float, P, I64, I64, I64,
+                                             P, I64, c_float, P, I64, I64, I64, P, P, P, c_size_t, P]),
     "mlora_combine": (c_int, [P, I64, P, c_int, P, I64, c_int, P, c_int, P, P]),
     "mlora_combine_backward": (c_int, [P, P, I64, P, c_int, P, I64, c_int, P, c_int, P, P, P]),
     "mlora_scale_rows": (c_int, [P, I64, I64, I64, P, c_int, P, P, I64, P]),

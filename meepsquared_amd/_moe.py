@@ -239,13 +239,16 @@ def routed_forward(experts, hidden_states, top_k_index, top_k_weights, factors):
         return _grouped.lora_linear(x, weight, _stack_scale(experts, name), offsets, experts.is_transposed,
                                     lhs, rhs, scaling, bias)
 
+    link = None
     if hidden_states.dtype == torch.bfloat16 and _grouped.gathered_product_fits(experts.gate_up_proj):
-        # the gate_up product reads its rows straight from hidden_states through perm
+        # the gate_up product reads its rows straight from hidden_states through perm; the link lets the
+        # SwiGLU backward below form this product's B gradient from the dgu it writes
         lhs, rhs, scaling = factors.get("gate_up_proj", (None, None, 1.0))
         bias = experts.gate_up_proj_bias if getattr(experts, "has_bias", False) else None
+        link = _grouped.GateUpLink()
         gate_up = _grouped.lora_linear_gathered(hidden_states, perm, inv, k, experts.gate_up_proj,
                                                 _stack_scale(experts, "gate_up_proj"), offsets, experts.is_transposed,
-                                                lhs, rhs, scaling, bias)
+                                                lhs, rhs, scaling, bias, link)
     else:
         gate_up = project(_Gather.apply(hidden_states, perm, inv, offsets, k), "gate_up_proj", "gate_up_proj_bias")
     down_bias = getattr(experts, "has_bias", False) and experts.down_proj_bias is not None
@@ -256,7 +259,7 @@ def routed_forward(experts, hidden_states, top_k_index, top_k_weights, factors):
         lhs, rhs, scaling = factors.get("down_proj", (None, None, 1.0))
         result = _grouped.swiglu_lora_linear_combined(gate_up, top_k_weights, perm, inv, k, experts.down_proj,
                                                       _stack_scale(experts, "down_proj"), offsets,
-                                                      experts.is_transposed, lhs, rhs, scaling)
+                                                      experts.is_transposed, lhs, rhs, scaling, link)
         assert result.shape[0] == num_tokens
         return result.to(hidden_states.dtype)
     # the model's own gate (autograd through its PyTorch operations on the GPU), or the SwiGLU kernel

@@ -69,6 +69,51 @@ __device__ __forceinline__ uint32_t f32_to_e4m3(float v) {
   return sign | (exp << 3) | ((b >> 20) & 7u);
 }
 
+// eight bf16 (one 16-byte vector) <-> eight floats
+__device__ __forceinline__ void unpack8(const u32x4& v, float* f) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = bf16_bits_to_f32(v[i] & 0xFFFFu);
+    f[2 * i + 1] = bf16_bits_to_f32(v[i] >> 16);
+  }
+}
+__device__ __forceinline__ u32x4 pack8(const float* f) {
+  u32x4 v;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = pack_bf16x2(f[2 * i], f[2 * i + 1]);
+  return v;
+}
+
+// a routing weight (bf16 or fp32) as fp32
+template <typename TW>
+__device__ __forceinline__ float load_w(const TW* w, int64_t i);
+template <>
+__device__ __forceinline__ float load_w<float>(const float* w, int64_t i) { return w[i]; }
+template <>
+__device__ __forceinline__ float load_w<bf16>(const bf16* w, int64_t i) { return (float)w[i]; }
+
+// ---- SwiGLU (TF integrations/moe.py:509-520: act = silu(gate) * up) ----
+__device__ __forceinline__ float sigmoidf_(float g) { return 1.0f / (1.0f + expf(-g)); }
+
+// SwiGLU's backward over eight columns of one row: gate gg, up u, the incoming gradient d taken with the
+// row's weight wt (dact = wt * d), zeros where !live.  act receives the forward's act values (bf16(silu *
+// up), as the forward kernel rounds them); returns sum_q d[q] * act[q] in column order.
+__device__ __forceinline__ float swiglu_grad8(const float* gg, const float* u, const float* d, float wt, bool live,
+                                              float* dg, float* du, float* act) {
+  float dot = 0.f;
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const float sg = sigmoidf_(gg[q]);
+    const float silu = gg[q] * sg;
+    act[q] = round_bf16(silu * u[q]);
+    dot += d[q] * act[q];
+    const float dd = wt * d[q];
+    du[q] = live ? dd * silu : 0.f;
+    dg[q] = live ? dd * u[q] * sg * (1.0f + gg[q] * (1.0f - sg)) : 0.f;
+  }
+  return dot;
+}
+
 // ---- wave primitives (wave64) ----
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

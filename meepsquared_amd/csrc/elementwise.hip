@@ -15,27 +15,6 @@
 
 namespace mlora {
 
-__device__ __forceinline__ void unpack8(const u32x4& v, float* f) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    f[2 * i] = bf16_bits_to_f32(v[i] & 0xFFFFu);
-    f[2 * i + 1] = bf16_bits_to_f32(v[i] >> 16);
-  }
-}
-__device__ __forceinline__ u32x4 pack8(const float* f) {
-  u32x4 v;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) v[i] = pack_bf16x2(f[2 * i], f[2 * i + 1]);
-  return v;
-}
-
-template <typename TW>
-__device__ __forceinline__ float load_w(const TW* w, int64_t i);
-template <>
-__device__ __forceinline__ float load_w<float>(const float* w, int64_t i) { return w[i]; }
-template <>
-__device__ __forceinline__ float load_w<bf16>(const bf16* w, int64_t i) { return (float)w[i]; }
-
 // ---- gather: one 16-byte vector per thread, grid-stride over (row, vector) ----
 __global__ __launch_bounds__(256) void gather_rows_kernel(const u32x4* __restrict__ h, int64_t ldh_v, int64_t Hv,
                                                           const int64_t* __restrict__ perm, int64_t S, int k,
@@ -107,8 +86,6 @@ __global__ __launch_bounds__(256) void gather_rows_backward_kernel(const u32x4* 
 }
 
 // ---- SwiGLU ----
-__device__ __forceinline__ float sigmoidf_(float g) { return 1.0f / (1.0f + expf(-g)); }
-
 __global__ __launch_bounds__(256) void swiglu_kernel(const u32x4* __restrict__ gu, int64_t S, int64_t Iv,
                                                      u32x4* __restrict__ act) {
   const int64_t total = S * Iv;
@@ -196,17 +173,8 @@ __global__ __launch_bounds__(256) void swiglu_backward_weighted_kernel(
       unpack8(vu[h], u);
       unpack8(vd[h], d);
       const bool live = p < valid;
-      const float wt = wrow[rr];
-      float dot = 0.f;
-#pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        const float sg = sigmoidf_(gg[q]);
-        const float silu = gg[q] * sg;
-        dot += d[q] * round_bf16(silu * u[q]);  // the forward's act value
-        const float dd = wt * d[q];
-        du[q] = live ? dd * silu : 0.f;
-        dg[q] = live ? dd * u[q] * sg * (1.0f + gg[q] * (1.0f - sg)) : 0.f;
-      }
+      float act[8];
+      const float dot = swiglu_grad8(gg, u, d, wrow[rr], live, dg, du, act);
       dgu[p * 2 * Iv + c] = pack8(dg);
       dgu[p * 2 * Iv + Iv + c] = pack8(du);
       sw_part[i] = dot;
