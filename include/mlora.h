@@ -307,6 +307,14 @@ int mlora_combine_backward(const void* dout, const void* y, int64_t H, const voi
 int mlora_scale_rows(const void* l, int64_t ldl, int64_t rows, int64_t R, const void* w, int w_dtype,
                      const int64_t* index, void* out, int64_t ldo, void* stream);
 
+/* The adapters' roles in the input-gradient product (src/meepsquared/_grouped.py:304-310, _Adapters.swapped)
+ * in one launch: at_out (E, R, N) contiguous = bt's transpose, bt_out (E, K, R) contiguous = at's transpose,
+ * for at = A^T (E, R, K) and bt = B^T (E, N, R) as mlora_grouped_gemm takes them (unit stride along K and
+ * R; strides at_se, at_sr, bt_se, bt_sn multiples of 8, 16-byte aligned).  R (the padded rank) 16 or 32,
+ * K and N multiples of 8 above R; other shapes take two mlora_transpose calls. */
+int mlora_swap_adapters(const void* at, int64_t at_se, int64_t at_sr, const void* bt, int64_t bt_se, int64_t bt_sn,
+                        int64_t E, int64_t R, int64_t K, int64_t N, void* at_out, void* bt_out, void* stream);
+
 /* dst[e][b][a] = src[e*s_e + a*s_a + b*s_b] (bf16): a batched transpose into a contiguous (E, B, A)
  * tensor, for the adapters' roles in the input-gradient product, which
  * src/meepsquared/_grouped.py:304-310 (_Adapters.swapped) addresses by strides. */

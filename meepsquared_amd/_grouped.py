@@ -143,8 +143,17 @@ class _Adapters:
         """The adapters of the input-gradient product: B takes A's role and A B's (_grouped.py:304-310)."""
         other = object.__new__(_Adapters)
         other.rank, other.padded = self.rank, self.padded
-        other.at = _transposed(self.bt)  # (e, R, n): B's rows become the new k
-        other.bt = _transposed(self.at)  # (e, k, R)
+        E, R, K = self.at.shape
+        N = self.bt.shape[1]
+        if R in (16, 32) and K > R and N > R and K % 8 == 0 and N % 8 == 0:  # both transposes in one launch
+            other.at = torch.empty((E, R, N), device=self.at.device, dtype=torch.bfloat16)
+            other.bt = torch.empty((E, K, R), device=self.at.device, dtype=torch.bfloat16)
+            call("mlora_swap_adapters", ptr(self.at), self.at.stride(0), self.at.stride(1), ptr(self.bt),
+                 self.bt.stride(0), self.bt.stride(1), E, R, K, N, ptr(other.at), ptr(other.bt),
+                 _lib.stream(self.at.device))
+        else:
+            other.at = _transposed(self.bt)  # (e, R, n): B's rows become the new k
+            other.bt = _transposed(self.at)  # (e, k, R)
         return other
 
 

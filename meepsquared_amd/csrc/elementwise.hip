@@ -585,12 +585,9 @@ __global__ __launch_bounds__(256) void transpose_vec_kernel(const bf16* __restri
 __device__ __forceinline__ uint32_t lo_halves(uint32_t x0, uint32_t x1) { return __builtin_amdgcn_perm(x1, x0, 0x05040100u); }
 __device__ __forceinline__ uint32_t hi_halves(uint32_t x0, uint32_t x1) { return __builtin_amdgcn_perm(x1, x0, 0x07060302u); }
 
-template <bool NB>  // NB: the source's columns (B) are the narrow side
-__global__ __launch_bounds__(64) void transpose_reg_kernel(const bf16* __restrict__ src, int64_t A, int64_t B,
-                                                           int64_t s_e, int64_t s_a, bf16* __restrict__ dst,
-                                                           int64_t items) {
-  const int64_t t = (int64_t)blockIdx.x * 64 + threadIdx.x;
-  if (t >= items) return;
+template <bool NB>  // NB: the source's columns (B) are the narrow side; item t of the transpose
+__device__ __forceinline__ void transpose_reg_item(const bf16* __restrict__ src, int64_t A, int64_t B, int64_t s_e,
+                                                   int64_t s_a, bf16* __restrict__ dst, int64_t t) {
   if constexpr (NB) {  // rows a0 .. a0+7, columns b0 .. b0+15 -> dst rows b0 .. b0+15, columns a0 .. a0+7
     const int64_t na = A / 8, nb = B / 16;
     const int64_t a0 = (t % na) * 8, rest = t / na, b0 = (rest % nb) * 16, e = rest / nb;
@@ -633,6 +630,30 @@ __global__ __launch_bounds__(64) void transpose_reg_kernel(const bf16* __restric
         *(u32x4*)(d + j * A + 8 * h) = o;
       }
     }
+  }
+}
+
+template <bool NB>
+__global__ __launch_bounds__(64) void transpose_reg_kernel(const bf16* __restrict__ src, int64_t A, int64_t B,
+                                                           int64_t s_e, int64_t s_a, bf16* __restrict__ dst,
+                                                           int64_t items) {
+  const int64_t t = (int64_t)blockIdx.x * 64 + threadIdx.x;
+  if (t < items) transpose_reg_item<NB>(src, A, B, s_e, s_a, dst, t);
+}
+
+// The adapters' two transposes for the input-gradient product in one launch: blocks below nb1 transpose
+// (E, N, R) -> (E, R, N) (the narrow side the source's columns), the others (E, R, K) -> (E, K, R).
+__global__ __launch_bounds__(64) void transpose_pair_kernel(const bf16* __restrict__ s1, int64_t A1, int64_t B1,
+                                                            int64_t se1, int64_t sa1, bf16* __restrict__ d1,
+                                                            int64_t items1, int64_t nb1, const bf16* __restrict__ s2,
+                                                            int64_t A2, int64_t B2, int64_t se2, int64_t sa2,
+                                                            bf16* __restrict__ d2, int64_t items2) {
+  if ((int64_t)blockIdx.x < nb1) {
+    const int64_t t = (int64_t)blockIdx.x * 64 + threadIdx.x;
+    if (t < items1) transpose_reg_item<true>(s1, A1, B1, se1, sa1, d1, t);
+  } else {
+    const int64_t t = ((int64_t)blockIdx.x - nb1) * 64 + threadIdx.x;
+    if (t < items2) transpose_reg_item<false>(s2, A2, B2, se2, sa2, d2, t);
   }
 }
 
@@ -708,4 +729,24 @@ extern "C" int mlora_transpose_u8(const void* src, int64_t E, int64_t A, int64_t
   hipLaunchKernelGGL(transpose_kernel<uint8_t>, dim3((unsigned)((B + 63) / 64), (unsigned)((A + 63) / 64), (unsigned)E),
                      dim3(256), 0, as_stream(stream), (const uint8_t*)src, A, B, s_e, s_a, s_b, (uint8_t*)dst);
   return launch_status("transpose_u8");
+}
+
+extern "C" int mlora_swap_adapters(const void* at, int64_t at_se, int64_t at_sr, const void* bt, int64_t bt_se,
+                                   int64_t bt_sn, int64_t E, int64_t R, int64_t K, int64_t N, void* at_out,
+                                   void* bt_out, void* stream) {
+  clear_error();
+  if (E < 1 || (R != 16 && R != 32) || K <= R || N <= R || K % 8 || N % 8)
+    return fail("swap_adapters: E=%lld, R=%lld, K=%lld, N=%lld: needs R 16 or 32 and K, N multiples of 8 above R",
+                (long long)E, (long long)R, (long long)K, (long long)N);
+  if (at_sr < K || at_sr % 8 || at_se % 8 || bt_sn < R || bt_sn % 8 || bt_se % 8 ||
+      (((uintptr_t)at | (uintptr_t)bt | (uintptr_t)at_out | (uintptr_t)bt_out) & 15u))
+    return fail("swap_adapters: the factors need 16-byte aligned rows and strides that are multiples of 8");
+  const int64_t items1 = E * (N / 8) * (R / 16), items2 = E * (R / 16) * (K / 8);
+  const int64_t nb1 = (items1 + 63) / 64, blocks = nb1 + (items2 + 63) / 64;
+  if (blocks > 0x7FFFFFFF) return fail("swap_adapters: (E=%lld, K=%lld, N=%lld) exceeds the grid", (long long)E,
+                                       (long long)K, (long long)N);
+  hipLaunchKernelGGL(transpose_pair_kernel, dim3((unsigned)blocks), dim3(64), 0, as_stream(stream), (const bf16*)bt, N,
+                     R, bt_se, bt_sn, (bf16*)at_out, items1, nb1, (const bf16*)at, R, K, at_se, at_sr, (bf16*)bt_out,
+                     items2);
+  return launch_status("swap_adapters");
 }

@@ -289,6 +289,22 @@ def test_the_batched_transpose_is_exact(E, A, B):
     assert torch.equal(_transposed(s), s.transpose(1, 2).contiguous())
 
 
+@pytest.mark.parametrize("rank,K,N", [(16, 2048, 1536), (12, 768, 2048), (20, 136, 200), (32, 40, 48)])
+def test_the_swapped_adapters_in_one_launch_are_the_transposes(rank, K, N):
+    """mlora_swap_adapters (both transposes of the input-gradient product's adapters in one launch, padded rank
+    16 or 32) gives exactly the two transposes."""
+    from meepsquared_amd import _grouped
+
+    torch.manual_seed(rank + K + N)
+    E = 7
+    lhs, rhs = torch.randn(E, N, rank, device="cuda"), torch.randn(E, rank, K, device="cuda")
+    a = _grouped._Adapters(lhs, rhs, False)
+    sw = a.swapped()
+    R = a.at.shape[1]
+    assert sw.at.shape == (E, R, N) and sw.bt.shape == (E, K, R)
+    assert torch.equal(sw.at, a.bt.transpose(1, 2)) and torch.equal(sw.bt, a.at.transpose(1, 2))
+
+
 def test_the_swapped_adapters_take_each_others_roles():
     from meepsquared_amd import _grouped
 
