@@ -1045,8 +1045,6 @@ __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_ker
       const bool tb = TALL && i == FM;
       if (tb ? !tall : i >= am) continue;
       const int rbase = tb ? BM : (i * WAVES_M + wm) * 32;
-      const int row = rbase + (lane & 31);
-      const uint32_t orow = (uint32_t)(row * p.ldo * 2);
 #pragma unroll
       for (int j = 0; j < FN; ++j) {
         if (j >= an || (tb && j != wm)) continue;
@@ -1065,9 +1063,9 @@ __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_ker
             }
           }
         }
-        // lane l holds columns 8g + 4(l/32) .. +3 of its row for g = 0..3; one swap of the lanes'
+        // lane l holds columns 8g + 4(l/32) .. +3 of row l % 32 for g = 0..3; one swap of the lanes'
         // halves per pair of groups gives lane l < 32 columns 16h .. 16h+7 and lane l + 32 columns
-        // 16h+8 .. 16h+15 (h = 0, 1): 16-byte stores, each row's 32 columns in two instructions
+        // 16h+8 .. 16h+15 (h = 0, 1)
         u32x2 pk[4];
         if (plain) {  // no stack scale, row scale or bias: one fma per value
 #pragma unroll
@@ -1103,13 +1101,27 @@ __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_ker
             pk[2 * h][d] = sw[0];
             pk[2 * h + 1][d] = sw[1];
           }
-        if (row >= mrows) continue;
+        // lane l < 32 now holds columns 0-7 (x) and 16-23 (y) of row l, lane l + 32 columns 8-15 and 24-31;
+        // in 16-lane rows, x = [r0-15 c0-7, r16-31 c0-7, r0-15 c8-15, r16-31 c8-15] and y likewise for
+        // c16-31.  A 32-lane swap then a 16-lane swap regroup them into a = [c0-7, c8-15, c16-23, c24-31] of
+        // rows 0-15 and b the same of rows 16-31: each store then writes 64 contiguous bytes of 16 rows
+        // (rows past the item's are dropped by the output's buffer range)
+        {
+          uint32_t xa[4] = {pk[0][0], pk[0][1], pk[1][0], pk[1][1]}, yb[4] = {pk[2][0], pk[2][1], pk[3][0], pk[3][1]};
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const int n = n0 + (j * WAVES_N + wn) * 32 + 16 * h + 8 * (lane >> 5);
-          if (n < p.N)
-            __builtin_amdgcn_raw_buffer_store_b128(u32x4{pk[2 * h][0], pk[2 * h][1], pk[2 * h + 1][0], pk[2 * h + 1][1]},
-                                                   ro, orow + (uint32_t)(n - n0) * 2 + (uint32_t)n0 * 2, 0, 0);
+          for (int q = 0; q < 4; ++q) {
+            const auto s1 = __builtin_amdgcn_permlane32_swap(xa[q], yb[q], false, false);
+            const auto s2 = __builtin_amdgcn_permlane16_swap(s1[0], s1[1], false, false);
+            xa[q] = s2[0];
+            yb[q] = s2[1];
+          }
+          const int n = n0 + (j * WAVES_N + wn) * 32 + 8 * (lane >> 4);
+          const uint32_t ora = (uint32_t)((rbase + (lane & 15)) * p.ldo * 2) + (uint32_t)n * 2;
+          if (n < p.N) {
+            __builtin_amdgcn_raw_buffer_store_b128(u32x4{xa[0], xa[1], xa[2], xa[3]}, ro, ora, 0, 0);
+            __builtin_amdgcn_raw_buffer_store_b128(u32x4{yb[0], yb[1], yb[2], yb[3]}, ro,
+                                                   ora + (uint32_t)(16 * p.ldo * 2), 0, 0);
+          }
         }
       }
     }

@@ -66,6 +66,8 @@ CASES = {
     "columns past a 64-column block": (520, 72, 4, [100, 160, 0, 250]),
     "config-1 shape": (8192, 768, 128, [64] * 128),
     "experts split over workgroups": (20480, 64, 4, [13030, 4000, 2000, 1450]),
+    "one expert, eight columns, rows not a multiple of 32": (77, 8, 1, [70]),
+    "every row a sentinel": (96, 128, 3, [0, 0, 0]),
 }
 
 
