@@ -93,7 +93,13 @@ template <>
 __device__ __forceinline__ float load_w<bf16>(const bf16* w, int64_t i) { return (float)w[i]; }
 
 // ---- SwiGLU (TF integrations/moe.py:509-520: act = silu(gate) * up) ----
-__device__ __forceinline__ float sigmoidf_(float g) { return 1.0f / (1.0f + expf(-g)); }
+// sigmoid(g) = 1 / (1 + e^-g) from the hardware's base-2 exponential and reciprocal (v_exp_f32, v_rcp_f32,
+// each within about 1 ulp of fp32): a few ulp of fp32 in all, far below the bf16 rounding every caller
+// applies to its results.  e^-g overflowing to +inf gives 0 (silu(g) = -0 for very negative g), as the
+// libm form does.
+__device__ __forceinline__ float sigmoidf_(float g) {
+  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g * -1.4426950408889634f));
+}
 
 // SwiGLU's backward over eight columns of one row: gate gg, up u, the incoming gradient d taken with the
 // row's weight wt (dact = wt * d), zeros where !live.  act receives the forward's act values (bf16(silu *

@@ -138,3 +138,46 @@ def test_the_layer_takes_the_fused_swiglu_backward_and_matches_the_two_reduction
     for i, (a, b) in enumerate(zip(got, want)):
         assert rel(a.float(), b.float()) < 1e-2, i
     assert got_counts.get("grouped_reduce", 0) == want_counts.get("grouped_reduce", 0) - 2, (got_counts, want_counts)
+
+
+def _bf16_ulp(v):
+    """The spacing of bf16 values at |v| (the smallest normal's spacing below it)."""
+    a = v.abs().clamp_min(2.0 ** -126)
+    return torch.exp2(torch.floor(torch.log2(a)) - 7)
+
+
+def test_swiglu_and_its_backward_are_within_one_bf16_step_of_the_exact_values():
+    """mlora_swiglu and mlora_swiglu_backward against silu(g)·u and its derivatives taken in float64 from
+    the same bf16 inputs, then rounded to bf16 once (TF integrations/moe.py:509-520): every value within
+    one bf16 step of the exact one, nearly all of them equal to it; gates from 0 and ±tiny to ±1e4, where
+    the sigmoid saturates or e^-g overflows."""
+    from meepsquared_amd import _lib
+    from meepsquared_amd._lib import call, ptr
+
+    g = torch.Generator(device="cuda").manual_seed(11)
+    S, I = 4096, 256
+    gate = torch.randn(S, I, device="cuda", generator=g) * 4
+    special = torch.tensor([0.0, -0.0, 1e-30, -1e-30, 1e-3, -1e-3, 15.0, -15.0, 88.0, -88.0, 90.0, -90.0,
+                            1e4, -1e4, 3.0, -3.0], device="cuda")
+    gate[:, :special.numel()] = special
+    gu = torch.cat([gate, torch.randn(S, I, device="cuda", generator=g) * 2], 1).bfloat16()
+    d = torch.randn(S, I, device="cuda", generator=g).bfloat16()
+    st = _lib.stream()
+    act = torch.empty(S, I, device="cuda", dtype=torch.bfloat16)
+    call("mlora_swiglu", ptr(gu), S, I, ptr(act), st)
+    dgu = torch.empty_like(gu)
+    call("mlora_swiglu_backward", ptr(gu), ptr(d), S, I, ptr(dgu), st)
+    torch.cuda.synchronize()
+
+    g64, u64, d64 = gu[:, :I].double(), gu[:, I:].double(), d.double()
+    sg = torch.sigmoid(g64)
+    want = {"act": g64 * sg * u64, "d_gate": d64 * u64 * sg * (1 + g64 * (1 - sg)), "d_up": d64 * g64 * sg}
+    got = {"act": act, "d_gate": dgu[:, :I], "d_up": dgu[:, I:]}
+    for name, w in want.items():
+        ours = got[name].double()
+        exact = w.bfloat16().double()
+        off = (ours - exact).abs()
+        # below 2^-100 fp32's e^-g has overflowed (g < -88.7): 0, as with libm's expf
+        assert bool(((off <= _bf16_ulp(exact)) | (w.abs() < 2.0 ** -100)).all()), (name, off.max().item())
+        # the random columns: a rounding of the fp32 chain lands past a bf16 midpoint only rarely
+        assert (off[:, special.numel():] != 0).double().mean().item() < 2e-3, name
