@@ -174,6 +174,24 @@ int mlora_grouped_gemm_gather_q(const void* x, int64_t ldx, int64_t x_rows, cons
                                 void* out, int64_t ldo, void* low, int64_t ldl, const int32_t* offsets, int E,
                                 void* stream);
 
+/* mlora_grouped_gemm_gather_q's forward product (no row scale, no scale along k) of a gate_up stack, N = 2 I
+ * columns (gate, then up), with SwiGLU formed in the same pass:
+ *   act[r, c] = bf16(g · sigmoid(g) · u),  g = out[r, c], u = out[r, I + c]  (the stored bf16 values),
+ * the values mlora_swiglu(out) writes, row stride lda (>= I, a multiple of 8, 16-byte aligned base).  out
+ * and low are written as mlora_grouped_gemm_gather_q writes them.  Needs N a multiple of 256, adapters of
+ * rank 16 or none, and a stack the DMA-fed product takes (bf16; fp8 and NF4 k contiguous).  Replaces, in the layer's forward,
+ * _grouped_gemm_kernel's gate_up launch and the SwiGLU pass after it (src/meepsquared/_moe.py:80-84,
+ * TF integrations/moe.py:509-520), so that gu is not read back. */
+int mlora_grouped_gemm_gather_swiglu(const void* x, int64_t ldx, int64_t x_rows, const int64_t* gather, int k,
+                                     int64_t rows, int K, int N, const void* w, int w_dtype, int64_t w_se,
+                                     int64_t w_sk, int64_t w_sn, const float* scale, int scale_kind, int64_t scale_se,
+                                     const uint8_t* nf4_absmax_q, const float* nf4_absmax2, const float* nf4_code2,
+                                     const float* nf4_offset, const float* nf4_code, const void* at, int64_t at_se,
+                                     int64_t at_sr, const void* bt, int64_t bt_se, int64_t bt_sn, int rank,
+                                     float scaling, const void* bias, int64_t bias_se, void* out, int64_t ldo,
+                                     void* low, int64_t ldl, void* act, int64_t lda, const int32_t* offsets, int E,
+                                     void* stream);
+
 /* Scratch bytes mlora_grouped_gemm_db needs for (rows, K, E): fp32 partial sums, 16 x K per 256-row tile
  * (E + rows / 256 + 1 tile slots; 16-byte aligned, contents on entry ignored). */
 size_t mlora_grouped_gemm_db_workspace_bytes(int64_t rows, int K, int E);

@@ -476,11 +476,22 @@ def gathered_product_fits(weight, products_fp8=None) -> bool:
             and weight.shape[2] % 16 == 0 and weight.data_ptr() % 16 == 0)
 
 
+def swiglu_fusable(N, rank=0, row_scale=None, backward=False) -> bool:
+    """Whether the gathered product of a gate_up stack (N = 2 I columns) forms SwiGLU in its epilogue
+    (mlora_grouped_gemm_gather_swiglu): asked for with MEEPSQUARED_FUSED_SWIGLU=1, and a forward product
+    without row scale, N a multiple of 256, adapters padded to rank 16 or none.  Off by default: on MI355X at
+    the Qwen3-shaped layer the fused epilogue adds about what the SwiGLU pass it replaces takes (+33 us to the
+    gate_up product against 46 us)."""
+    return (os.environ.get("MEEPSQUARED_FUSED_SWIGLU", "0") == "1" and not backward and row_scale is None
+            and N % 256 == 0 and N > 0 and rank in (0, 16))
+
+
 def _launch_gathered(src, perm, k, weight, scale, offsets, is_transposed, adapters, scaling, bias,
-                     row_scale=None, backward=False):
+                     row_scale=None, backward=False, swiglu=False):
     """One launch of the product over the rows src[perm // k]: (out, low).  row_scale: output row r multiplied
     by row_scale[perm[r]] (low stays bf16 of the unscaled rows' x·A).  A bf16, fp8 (bf16 products) or NF4
-    stack, as gathered_product_fits admits."""
+    stack, as gathered_product_fits admits.  swiglu (swiglu_fusable must hold): (out, low, act), act = SwiGLU
+    of out formed in the same launch, the values mlora_swiglu(out) gives."""
     _lib.require_gpu(src, perm, offsets)
     if not gathered_product_fits(weight, False):
         raise TypeError(f"the gathered product takes a bf16, fp8 e4m3 or NF4 stack with rows of whole 16-byte chunks, "
@@ -492,8 +503,12 @@ def _launch_gathered(src, perm, k, weight, scale, offsets, is_transposed, adapte
     out = torch.empty((rows, N), device=src.device, dtype=torch.bfloat16)
     R = adapters.padded if adapters is not None else 0
     low = torch.empty((rows, R), device=src.device, dtype=torch.bfloat16) if adapters is not None else None
+    if swiglu and not swiglu_fusable(N, R, row_scale, backward):
+        raise ValueError(f"the gathered product forms SwiGLU for a forward product of N % 256 == 0 columns and "
+                         f"adapters of rank 16 or none, not N={N}, rank {R}")
+    act = torch.empty((rows, N // 2), device=src.device, dtype=torch.bfloat16) if swiglu else None
     if rows == 0:
-        return out, low
+        return (out, low, act) if swiglu else (out, low)
     if (isinstance(weight, torch.Tensor) and weight.dtype == torch.bfloat16
             and _scale_args(scale, weight, backward, is_transposed)[3]):
         # a per-row scale along k is applied by the fp8 decode only
@@ -508,6 +523,17 @@ def _launch_gathered(src, perm, k, weight, scale, offsets, is_transposed, adapte
     info = {"rows": rows, "K": K, "N": N, "rank": adapters.rank if adapters is not None else 0}
     if launch_observer is not None:
         launch_observer("grouped_gemm", "before", info)
+    if swiglu:
+        call("mlora_grouped_gemm_gather_swiglu", ptr(src), src.stride(0), T, ptr(perm), k, rows, K, N,
+             w_ptr, w_dtype, w_se, w_sk, w_sn, ptr(scale_), scale_kind, scale_se, *nf4,
+             ptr(at), at.stride(0) if at is not None else 0, at.stride(1) if at is not None else 0,
+             ptr(bt), bt.stride(0) if bt is not None else 0, bt.stride(1) if bt is not None else 0,
+             R, float(scaling), ptr(bias), bias.stride(0) if bias is not None else 0,
+             ptr(out), out.stride(0), ptr(low), low.stride(0) if low is not None else 0, ptr(act), act.stride(0),
+             ptr(offsets), offsets.numel(), _lib.stream(src.device))
+        if launch_observer is not None:
+            launch_observer("grouped_gemm", "after", info)
+        return out, low, act
     call("mlora_grouped_gemm_gather_q", ptr(src), src.stride(0), T, ptr(perm), k, ptr(row_scale),
          _lib.dtype_code(row_scale.dtype) if row_scale is not None else 0, rows, K, N,
          w_ptr, w_dtype, w_se, w_sk, w_sn, ptr(scale_), scale_kind, scale_se, on_k, *nf4,
@@ -589,16 +615,28 @@ def _launch_db(src, weight, scale, offsets, is_transposed, adapters, scaling, l,
 
 
 class GateUpLink:
-    """What the layer's two Functions share so that the SwiGLU backward also forms the gate_up adapter's B
+    """What the layer's two Functions share.  Forward: with want_act, the gate_up product forms SwiGLU in its
+    epilogue and leaves act here, and the down Function takes it when its input is that very gu, unchanged
+    (else it runs SwiGLU itself).  Backward, so that the SwiGLU backward also forms the gate_up adapter's B
     gradient (mlora_swiglu_backward_reduce): the gate_up product's forward leaves its low rows and scaling
     here, the down Function's backward leaves that gradient and the dgu it was formed from, and the gate_up
     backward takes it when its incoming gradient is that very dgu (else it reduces as usual)."""
 
-    __slots__ = ("low", "scaling", "transposed", "padded", "grad_b", "dgu", "dgu_version")
+    __slots__ = ("low", "scaling", "transposed", "padded", "grad_b", "dgu", "dgu_version", "want_act", "act",
+                 "act_of", "act_version")
 
-    def __init__(self):
-        self.low = self.grad_b = self.dgu = None
-        self.scaling, self.transposed, self.padded, self.dgu_version = 1.0, False, 0, -1
+    def __init__(self, want_act=False):
+        self.low = self.grad_b = self.dgu = self.act = self.act_of = None
+        self.scaling, self.transposed, self.padded, self.dgu_version, self.act_version = 1.0, False, 0, -1, -1
+        self.want_act = want_act
+
+    def take_act(self, gu):
+        """SwiGLU of gu formed by the gate_up product, or None."""
+        act, of = self.act, self.act_of
+        self.act = self.act_of = None
+        if act is None or gu is not of or gu._version != self.act_version:
+            return None
+        return act
 
     def take(self, grad_out):
         """The B gradient formed for grad_out, or None."""
@@ -621,7 +659,14 @@ class _GatheredLoraProduct(torch.autograd.Function):
             else hidden.contiguous()
         offsets = offsets.to(torch.int32).contiguous()
         adapters = _Adapters(lhs, rhs, is_transposed) if lhs is not None else None
-        out, low = _launch_gathered(hidden, perm, k, weight, scale, offsets, is_transposed, adapters, scaling, bias)
+        N = _stack_strides(weight, hidden.shape[1], is_transposed)[0]
+        if link is not None and link.want_act and swiglu_fusable(N, adapters.padded if adapters is not None else 0):
+            out, low, act = _launch_gathered(hidden, perm, k, weight, scale, offsets, is_transposed, adapters, scaling,
+                                             bias, swiglu=True)
+            link.act, link.act_of, link.act_version = act, out, out._version
+        else:
+            out, low = _launch_gathered(hidden, perm, k, weight, scale, offsets, is_transposed, adapters, scaling,
+                                        bias)
         ctx.save_for_backward(hidden, perm, inv, offsets, *((low,) if low is not None else ()))
         ctx.link = link
         if link is not None and adapters is not None:
@@ -746,10 +791,12 @@ class _SwigluCombinedLoraProduct(torch.autograd.Function):
     @staticmethod
     def forward(ctx, gu, weights, perm, inv, k, weight, scale, offsets, is_transposed, lhs, rhs, scaling, link=None):
         offsets = offsets.to(torch.int32).contiguous()
+        act = link.take_act(gu) if link is not None else None  # (formed by the gate_up product)
         gu = gu.contiguous()
         S, I2 = gu.shape
-        act = torch.empty((S, I2 // 2), device=gu.device, dtype=gu.dtype)
-        call("mlora_swiglu", ptr(gu), S, I2 // 2, ptr(act), _lib.stream(gu.device))
+        if act is None:
+            act = torch.empty((S, I2 // 2), device=gu.device, dtype=gu.dtype)
+            call("mlora_swiglu", ptr(gu), S, I2 // 2, ptr(act), _lib.stream(gu.device))
         adapters = _Adapters(lhs, rhs, is_transposed) if lhs is not None else None
         y, low = _launch(act, weight, scale, offsets, is_transposed, adapters, scaling, None, True)
         H = y.shape[1]

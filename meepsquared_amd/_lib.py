@@ -45,6 +45,11 @@ SIGNATURES = {
                                             P, P, P, P, P,
                                             P, I64, I64, P, I64, I64, c_int, c_float, P, I64,
                                             P, I64, P, I64, P, c_int, P]),
+    "mlora_grouped_gemm_gather_swiglu": (c_int, [P, I64, I64, P, c_int, I64, c_int, c_int,
+                                                 P, c_int, I64, I64, I64, P, c_int, I64,
+                                                 P, P, P, P, P,
+                                                 P, I64, I64, P, I64, I64, c_int, c_float, P, I64,
+                                                 P, I64, P, I64, P, I64, P, c_int, P]),
     "mlora_grouped_gemm_db_workspace_bytes": (c_size_t, [I64, c_int, c_int]),
     "mlora_grouped_gemm_db": (c_int, [P, I64, I64, P, c_int, P, c_int, I64, c_int, c_int,
                                       P, I64, I64, I64, P, c_int, I64,

@@ -240,19 +240,21 @@ def routed_forward(experts, hidden_states, top_k_index, top_k_weights, factors):
                                     lhs, rhs, scaling, bias)
 
     link = None
+    down_bias = getattr(experts, "has_bias", False) and experts.down_proj_bias is not None
+    swiglu_combined = custom_gate is None and _grouped.gathered_product_fits(experts.down_proj) and not down_bias
     if hidden_states.dtype == torch.bfloat16 and _grouped.gathered_product_fits(experts.gate_up_proj):
-        # the gate_up product reads its rows straight from hidden_states through perm; the link lets the
-        # SwiGLU backward below form this product's B gradient from the dgu it writes
+        # the gate_up product reads its rows straight from hidden_states through perm; the link hands the
+        # SwiGLU it forms in its epilogue to the down Function below, and lets that Function's SwiGLU
+        # backward form this product's B gradient from the dgu it writes
         lhs, rhs, scaling = factors.get("gate_up_proj", (None, None, 1.0))
         bias = experts.gate_up_proj_bias if getattr(experts, "has_bias", False) else None
-        link = _grouped.GateUpLink()
+        link = _grouped.GateUpLink(want_act=swiglu_combined)
         gate_up = _grouped.lora_linear_gathered(hidden_states, perm, inv, k, experts.gate_up_proj,
                                                 _stack_scale(experts, "gate_up_proj"), offsets, experts.is_transposed,
                                                 lhs, rhs, scaling, bias, link)
     else:
         gate_up = project(_Gather.apply(hidden_states, perm, inv, offsets, k), "gate_up_proj", "gate_up_proj_bias")
-    down_bias = getattr(experts, "has_bias", False) and experts.down_proj_bias is not None
-    if custom_gate is None and _grouped.gathered_product_fits(experts.down_proj) and not down_bias:
+    if swiglu_combined:
         # SwiGLU, the down product and the combine as one Function: its backward reads the output
         # gradient through perm, and the SwiGLU backward applies the combine weights and forms their
         # gradient (y is not kept)

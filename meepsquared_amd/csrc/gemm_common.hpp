@@ -54,6 +54,13 @@ struct GemmArgs {
   float* dbw;
   bf16* dbo;                 // the gradient (experts, K, 16) by its strides, written by the finishing launch
   int64_t dbo_se, dbo_sk, dbo_sr;
+  // SwiGLU of the product fused into its epilogue (the DMA-fed product): NULL act, or N = 2 swi columns
+  // (gate, then up) and act[row][c] = bf16(silu(out[row][c]) · out[row][swi + c]) of the stored bf16 values,
+  // row stride lda.  Each 256-column tile then holds 128 gate columns and the 128 up columns that pair with
+  // them.
+  bf16* act;
+  int64_t lda;
+  int swi;
 };
 
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
@@ -138,6 +145,8 @@ int launch_grouped_gemm_bf16(const GemmArgs& a, bool k_contiguous, hipStream_t s
 // the fused adapter gradient's workspace rows of 16 x K fp32 (one per tile), and its expert limit
 int64_t grouped_gemm_db_slots(int64_t rows, int E);
 int grouped_gemm_db_max_experts();
+// whether the DMA-fed product's tile shape pairs gate and up columns for the fused SwiGLU (GemmArgs::act)
+bool grouped_gemm_swiglu_fits();
 // the DMA-fed product for a quantised stack read with k contiguous (decoded in registers)
 bool grouped_gemm_dma_takes(const GemmArgs& a, int w_dtype, bool k_contiguous, bool scale_on_k);
 int launch_grouped_gemm_dma_q(const GemmArgs& a, int w_dtype, bool scale_on_k, hipStream_t s);

@@ -585,7 +585,13 @@ struct DbIn {
   size_t workspace_bytes;
 };
 
-static int grouped_gemm_impl(const DbIn* db, const void* x, int64_t ldx, const int64_t* gather, int gk, int64_t xrows,
+// The fused SwiGLU's output (mlora_grouped_gemm_gather_swiglu)
+struct SwiOut {
+  void* act;
+  int64_t lda;
+};
+
+static int grouped_gemm_impl(const DbIn* db, const SwiOut* so, const void* x, int64_t ldx, const int64_t* gather, int gk, int64_t xrows,
                              const void* row_scale, int row_scale_dt, int64_t rows, int K, int N, const void* w,
                              int w_dtype,
                                   int64_t w_se, int64_t w_sk, int64_t w_sn, const float* scale, int scale_kind,
@@ -668,6 +674,15 @@ static int grouped_gemm_impl(const DbIn* db, const void* x, int64_t ldx, const i
     if (db->workspace == nullptr || db->workspace_bytes < need || !aligned(db->workspace, 16))
       return fail("grouped_gemm_db: workspace of %zu bytes, %zu needed (16-byte aligned)", db->workspace_bytes, need);
   }
+  if (so != nullptr) {
+    if (db != nullptr) return fail("grouped_gemm_swiglu: no fused adapter gradient with the fused SwiGLU");
+    if (!grouped_gemm_swiglu_fits()) return fail("grouped_gemm_swiglu: this build's tile shape does not pair gate and up columns");
+    if (N % 256) return fail("grouped_gemm_swiglu: N=%d (gate and up) must be a multiple of 256", N);
+    if (so->act == nullptr || so->lda < N / 2 || so->lda % 8 || !aligned(so->act, 16))
+      return fail("grouped_gemm_swiglu: act needs a 16-byte aligned base and a row stride (%lld) that is a multiple of 8 "
+                  "and >= N/2", (long long)so->lda);
+    if ((int64_t)BM * so->lda * 2 > 0x7FFFFFF0) return fail("grouped_gemm_swiglu: act row stride %lld too large", (long long)so->lda);
+  }
   if (rows == 0 && db == nullptr) return 0;  // (with the fused gradient, the launch writes its zeros)
 
   GemmArgs g{};
@@ -690,6 +705,12 @@ static int grouped_gemm_impl(const DbIn* db, const void* x, int64_t ldx, const i
     g.dbl = (const bf16*)db->l; g.dbl_ld = db->ldl;
     g.dbw = (float*)db->workspace;
     g.dbo = (bf16*)db->out; g.dbo_se = db->o_se; g.dbo_sk = db->o_sk; g.dbo_sr = db->o_sr;
+  }
+  if (so != nullptr) {
+    g.act = (bf16*)so->act; g.lda = so->lda; g.swi = N / 2;
+    if (w_dtype != MLORA_DT_BF16 && !grouped_gemm_dma_takes(g, w_dtype, bkc, scale_k))
+      return fail("grouped_gemm_swiglu: the fused SwiGLU needs a stack the DMA-fed product takes (k contiguous, "
+                  "16-byte aligned rows; NF4: rows of whole 64-code blocks)");
   }
   hipStream_t s = as_stream(stream);
   // gathered rows are read by the DMA-fed product only (every stack type it takes)
@@ -720,7 +741,7 @@ extern "C" int mlora_grouped_gemm(const void* x, int64_t ldx, int64_t rows, int 
                                   const void* bt, int64_t bt_se, int64_t bt_sn, int rank, float scaling,
                                   const void* bias, int64_t bias_se, void* out, int64_t ldo, void* low, int64_t ldl,
                                   const int32_t* offsets, int E, void* stream) {
-  return grouped_gemm_impl(nullptr, x, ldx, nullptr, 1, rows, nullptr, 0, rows, K, N, w, w_dtype, w_se, w_sk, w_sn, scale,
+  return grouped_gemm_impl(nullptr, nullptr, x, ldx, nullptr, 1, rows, nullptr, 0, rows, K, N, w, w_dtype, w_se, w_sk, w_sn, scale,
                            scale_kind,
                            scale_se, scale_on_k, nf4_absmax_q, nf4_absmax2, nf4_code2, nf4_offset, nf4_code, at, at_se,
                            at_sr, bt, bt_se, bt_sn, rank, scaling, bias, bias_se, out, ldo, low, ldl, offsets, E, stream);
@@ -737,7 +758,7 @@ extern "C" int mlora_grouped_gemm_gather(const void* x, int64_t ldx, int64_t x_r
     clear_error();
     return fail("grouped_gemm_gather: gather is NULL");
   }
-  return grouped_gemm_impl(nullptr, x, ldx, gather, k, x_rows, row_scale, row_scale_dtype, rows, K, N, w, w_dtype, w_se, w_sk,
+  return grouped_gemm_impl(nullptr, nullptr, x, ldx, gather, k, x_rows, row_scale, row_scale_dtype, rows, K, N, w, w_dtype, w_se, w_sk,
                            w_sn, scale, scale_kind,
                            scale_se, 0, nullptr, nullptr, nullptr, nullptr, nullptr, at, at_se, at_sr, bt, bt_se, bt_sn,
                            rank, scaling, bias, bias_se, out, ldo, low, ldl, offsets, E, stream);
@@ -757,10 +778,31 @@ extern "C" int mlora_grouped_gemm_gather_q(const void* x, int64_t ldx, int64_t x
     clear_error();
     return fail("grouped_gemm_gather_q: gather is NULL");
   }
-  return grouped_gemm_impl(nullptr, x, ldx, gather, k, x_rows, row_scale, row_scale_dtype, rows, K, N, w, w_dtype,
+  return grouped_gemm_impl(nullptr, nullptr, x, ldx, gather, k, x_rows, row_scale, row_scale_dtype, rows, K, N, w, w_dtype,
                            w_se, w_sk, w_sn, scale, scale_kind, scale_se, scale_on_k, nf4_absmax_q, nf4_absmax2,
                            nf4_code2, nf4_offset, nf4_code, at, at_se, at_sr, bt, bt_se, bt_sn, rank, scaling, bias,
                            bias_se, out, ldo, low, ldl, offsets, E, stream);
+}
+
+extern "C" int mlora_grouped_gemm_gather_swiglu(const void* x, int64_t ldx, int64_t x_rows, const int64_t* gather, int k,
+                                                 int64_t rows, int K, int N, const void* w, int w_dtype, int64_t w_se,
+                                                 int64_t w_sk, int64_t w_sn, const float* scale, int scale_kind,
+                                                 int64_t scale_se, const uint8_t* nf4_absmax_q,
+                                                 const float* nf4_absmax2, const float* nf4_code2,
+                                                 const float* nf4_offset, const float* nf4_code, const void* at,
+                                                 int64_t at_se, int64_t at_sr, const void* bt, int64_t bt_se,
+                                                 int64_t bt_sn, int rank, float scaling, const void* bias,
+                                                 int64_t bias_se, void* out, int64_t ldo, void* low, int64_t ldl,
+                                                 void* act, int64_t lda, const int32_t* offsets, int E, void* stream) {
+  if (gather == nullptr) {
+    clear_error();
+    return fail("grouped_gemm_gather_swiglu: gather is NULL");
+  }
+  const SwiOut so{act, lda};
+  return grouped_gemm_impl(nullptr, &so, x, ldx, gather, k, x_rows, nullptr, 0, rows, K, N, w, w_dtype, w_se, w_sk,
+                           w_sn, scale, scale_kind, scale_se, 0, nf4_absmax_q, nf4_absmax2, nf4_code2, nf4_offset,
+                           nf4_code, at, at_se, at_sr, bt, bt_se, bt_sn, rank, scaling, bias, bias_se, out, ldo, low,
+                           ldl, offsets, E, stream);
 }
 
 extern "C" size_t mlora_grouped_gemm_db_workspace_bytes(int64_t rows, int K, int E) {
@@ -786,7 +828,7 @@ extern "C" int mlora_grouped_gemm_db(const void* x, int64_t ldx, int64_t x_rows,
     }
     x_rows = rows;
   }
-  return grouped_gemm_impl(&db, x, ldx, gather, k, x_rows, row_scale, row_scale_dtype, rows, K, N, w, MLORA_DT_BF16,
+  return grouped_gemm_impl(&db, nullptr, x, ldx, gather, k, x_rows, row_scale, row_scale_dtype, rows, K, N, w, MLORA_DT_BF16,
                            w_se, w_sk, w_sn, scale, scale_kind, scale_se, 0, nullptr, nullptr, nullptr, nullptr,
                            nullptr, at, at_se, at_sr, bt, bt_se, bt_sn, rank, scaling, bias, bias_se, out, ldo, low,
                            ldl, offsets, E, stream);

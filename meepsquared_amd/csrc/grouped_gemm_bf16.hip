@@ -74,6 +74,17 @@ constexpr int kSmallLastE = 1024;  // experts up to which the small last tiles a
 // by the copy latency).  The extra rows' x tile sits at the end of each ring slot.
 constexpr int XR = 32;
 
+// The product's column (the stack's row) at column c of the tile whose first column is n0.  With SwiGLU
+// fused (swi = half the columns), tile t's first half is gate columns 128 t .. and its second half the up
+// columns swi + 128 t .. that pair with them, so that each wave's two 32-column blocks j = 0, 1 hold a gate
+// block and its up block in the same lanes.
+template <bool SWI>
+__device__ __forceinline__ int tile_col(const GemmArgs& p, int n0, int c) {
+  if constexpr (!SWI) return n0 + c;
+  else return c < BN / 2 ? (n0 >> 1) + c : p.swi + (n0 >> 1) + (c - BN / 2);
+}
+constexpr bool kSwiOn = FN == 2 && WAVES_N * 64 == BN;  // the pairing above needs these shapes
+
 // [row][k] tiles (rows of BK bf16, CPR chunks of 16 bytes): chunk c of row r in slot c ^ f(r), with f
 // spreading the 16 rows one MFMA operand read touches over 16 distinct 16-byte bank groups
 __device__ __forceinline__ int swz_f(int row) { return (row >> (CPR == 4 ? 2 : 1)) & (CPR - 1); }
@@ -226,7 +237,7 @@ struct SlotSize {
 // copy's scalar offset, with no per-lane test; only a stage that crosses the end of K re-derives each
 // lane's k from its lane index and sends the lanes past K out of range (zeros).  Stack columns past N
 // are read like the others (inside the stack's buffer range, or zeros past its end) and never stored.
-template <bool BKC, int NRB, int WT, bool TALL = false, bool DB = false>
+template <bool BKC, int NRB, int WT, bool TALL = false, bool DB = false, bool SWI = false>
 struct Feed {
   static_assert(WT == kWBf16 || BKC, "fp8 and NF4 stacks are read with k contiguous");
   static_assert(!DB || (WT == kWBf16 && NRB == 1 && STAGES == 2), "the fused adapter gradient: bf16, rank 16, two slots");
@@ -322,16 +333,16 @@ struct Feed {
       if constexpr (WT != kWBf16) {  // [n][k] bytes: fp8 one per k, NF4 one per two k
         constexpr int CH = WTile<WT>::Chunks;
         const int row = ci / CH, c = (ci % CH) ^ swz_q<WT>(row);
-        const int n = n0 + row;
+        const int n = tile_col<SWI>(p, n0, row);
         const int64_t rowb = WTile<WT>::kFp8 ? (int64_t)n * p.w_sn : (int64_t)n * p.w_sn / 2;
         wo[q] = (uint32_t)(rowb + c * 16);
       } else if constexpr (BKC) {  // [n][k]
         const int row = ci / CPR, c = (ci % CPR) ^ swz_f(row);
-        const int n = n0 + row;
+        const int n = tile_col<SWI>(p, n0, row);
         wo[q] = (uint32_t)(((int64_t)n * p.w_sn + c * 8) * 2);
       } else {  // [k][n]
         const int kr = ci / (BN / 8), c = (ci % (BN / 8)) ^ ((kr & 3) << 2);
-        const int n = n0 + c * 8;
+        const int n = tile_col<SWI>(p, n0, c * 8);
         wo[q] = (uint32_t)(((int64_t)kr * p.w_sk + n) * 2);
       }
       wd[q] = BM * BK + instr * 512;
@@ -408,7 +419,7 @@ struct Feed {
     }
     if constexpr (PART == 1 && WT == kWNf4T) {  // waves 0 .. BN/64 - 1: one row of the absmax tile each
       if (wave_ < BN / 64) {
-        const int nbg = n0_ / 64 + wave_;
+        const int nbg = tile_col<SWI>(p, n0_, wave_ * 64) / 64;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
             rs, (lds_void*)(slot + BM * BK + WTile<WT>::Bytes / 2 + wave_ * BK * 2), 4,
             nbg < p.N / 64 && k0 + lane_ < p.K ? (uint32_t)(((int64_t)nbg * p.K + k0 + lane_) * 4) : kOob, 0, 0, 0);
@@ -547,10 +558,11 @@ struct Nf4Pipe {
       pl[3][m] = __builtin_amdgcn_perm(h23, h01, 0x07060302u);
     }
   }
+  template <bool SWI>
   __device__ __forceinline__ void init(const GemmArgs& p, int e, int n0, int wn, int lane) {
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
-      const int n = n0 + (j * WAVES_N + wn) * 32 + (lane & 31);
+      const int n = tile_col<SWI>(p, n0, (j * WAVES_N + wn) * 32 + (lane & 31));
       blk[j] = n < p.N ? ((int64_t)e * p.w_se + (int64_t)n * p.w_sn) >> 6 : -1;
     }
   }
@@ -797,7 +809,48 @@ __device__ __forceinline__ void kloop(const GemmArgs& p, const F& f, bf16* const
   }
 }
 
-template <bool BKC, int NRB, int WT, bool TALL = false, bool DB = false>
+// One 32 x 32 block of bf16 results (rows rbase .., columns col ..) from the MFMA layout: lane l holds
+// columns 8g + 4(l/32) .. +3 of row l % 32 in v[g], g = 0..3.  One swap of the lanes' halves per pair of
+// groups gives lane l < 32 columns 0-7 (x) and 16-23 (y) of row l, lane l + 32 columns 8-15 and 24-31; in
+// 16-lane rows, x = [r0-15 c0-7, r16-31 c0-7, r0-15 c8-15, r16-31 c8-15] and y likewise for c16-31.  A
+// 32-lane swap then a 16-lane swap regroup them into a = [c0-7, c8-15, c16-23, c24-31] of rows 0-15 and b
+// the same of rows 16-31: each store writes 64 contiguous bytes of 16 rows.  Rows past the resource's
+// range are dropped by it; columns from ncols on are not stored.
+__device__ __forceinline__ void store_block32(const u32x2 (&v)[4], rsrc_t r, int rbase, int64_t ld, int col,
+                                              int ncols, int lane) {
+  u32x2 pk[4] = {v[0], v[1], v[2], v[3]};
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int d = 0; d < 2; ++d) {
+      const auto sw = __builtin_amdgcn_permlane32_swap(pk[2 * h][d], pk[2 * h + 1][d], false, false);
+      pk[2 * h][d] = sw[0];
+      pk[2 * h + 1][d] = sw[1];
+    }
+  uint32_t xa[4] = {pk[0][0], pk[0][1], pk[1][0], pk[1][1]}, yb[4] = {pk[2][0], pk[2][1], pk[3][0], pk[3][1]};
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const auto s1 = __builtin_amdgcn_permlane32_swap(xa[q], yb[q], false, false);
+    const auto s2 = __builtin_amdgcn_permlane16_swap(s1[0], s1[1], false, false);
+    xa[q] = s2[0];
+    yb[q] = s2[1];
+  }
+  const int n = col + 8 * (lane >> 4);
+  const uint32_t o = (uint32_t)((rbase + (lane & 15)) * ld * 2) + (uint32_t)n * 2;
+  if (n < ncols) {
+    __builtin_amdgcn_raw_buffer_store_b128(u32x4{xa[0], xa[1], xa[2], xa[3]}, r, o, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b128(u32x4{yb[0], yb[1], yb[2], yb[3]}, r, o + (uint32_t)(16 * ld * 2), 0, 0);
+  }
+}
+
+// SwiGLU of two packed bf16 gate values and their up values, as mlora_swiglu computes each one
+__device__ __forceinline__ uint32_t swiglu_bf16x2(uint32_t g2, uint32_t u2) {
+  const float g0 = bf16_bits_to_f32(g2 & 0xFFFFu), g1 = bf16_bits_to_f32(g2 >> 16);
+  const float u0 = bf16_bits_to_f32(u2 & 0xFFFFu), u1 = bf16_bits_to_f32(u2 >> 16);
+  return pack_bf16x2(g0 * sigmoidf_(g0) * u0, g1 * sigmoidf_(g1) * u1);
+}
+
+template <bool BKC, int NRB, int WT, bool TALL = false, bool DB = false, bool SWI = false>
 __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_kernel(GemmArgs p) {
   constexpr int RP = NRB * 16;
   constexpr int LP = RP + 8;
@@ -871,7 +924,7 @@ __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_ker
     const int am = min(FM, max(0, (mb - wm + WAVES_M - 1) / WAVES_M));
     const int an = min(FN, max(0, (nbk - wn + WAVES_N - 1) / WAVES_N));
 
-    Feed<BKC, NRB, WT, TALL, DB> f;
+    Feed<BKC, NRB, WT, TALL, DB, SWI> f;
     f.rx = p.gather == nullptr ? make_rsrc(p.x + row0 * p.ldx, (int64_t)mrows * p.ldx * 2)
                                : make_rsrc(p.x, p.xrows * p.ldx * 2);
     {
@@ -904,7 +957,7 @@ __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_ker
     Nf4Pipe nf;
     if constexpr (WT == kWNf4T) nf.planes(code);  // (the tile map's barrier published the code book)
     if constexpr (WT == kWNf4) {
-      nf.init(p, e, n0, wn, lane);
+      nf.template init<SWI>(p, e, n0, wn, lane);
       nf.load(p, 0);
     }
     __syncthreads();  // the previous item's epilogue is done with the LDS
@@ -912,7 +965,7 @@ __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_ker
       static_assert(BN * 2 <= kThreads, "one chunk of the B^T tile per thread");
       if (p.scaling != 0.f && tid < BN * 2) {
         const rsrc_t rbt = make_rsrc(p.bt + (int64_t)e * p.bt_se, (int64_t)p.N * p.bt_sn * 2);
-        const int row = tid >> 1, half = (tid & 1) ^ ((row >> 2) & 1), n = n0 + row;
+        const int row = tid >> 1, half = (tid & 1) ^ ((row >> 2) & 1), n = tile_col<SWI>(p, n0, row);
         dma16(rbt, lbt + (tid >> 6) * 512, n < p.N ? (uint32_t)((n * p.bt_sn + half * 8) * 2) : kOob);
       }
     }
@@ -974,7 +1027,7 @@ __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_ker
     const bool col_scale = p.scale_kind == MLORA_SCALE_ROW && WT != kWFp8K, has_bias = p.bias != nullptr;
     const float cexp = p.scale_kind == MLORA_SCALE_EXPERT ? p.scale[e] : 1.f;
     if (tid < BN && (col_scale || has_bias)) {
-      const int n = n0 + tid;
+      const int n = tile_col<SWI>(p, n0, tid);
       if (col_scale) Lc[tid] = n < p.N ? p.scale[(int64_t)e * p.scale_se + n] : 0.f;
       if (has_bias) Lbias[tid] = n < p.N ? p.bias[(int64_t)e * p.bias_se + n] : (bf16)0.f;
     }
@@ -1019,7 +1072,7 @@ __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_ker
         const rsrc_t rbt = make_rsrc(p.bt + (int64_t)e * p.bt_se, (int64_t)p.N * p.bt_sn * 2);
         for (int c = tid; c < BN * RP / 8; c += kThreads) {
           const int nn = c / (RP / 8), rc = (c - nn * (RP / 8)) * 8;
-          const int n = n0 + nn;
+          const int n = tile_col<SWI>(p, n0, nn);
           *(u32x4*)(Lb + nn * LP + rc) = ld128(rbt, n < p.N ? (uint32_t)((n * p.bt_sn + rc) * 2) : kOob);
         }
       }
@@ -1038,6 +1091,18 @@ __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_ker
     const bool plain = !col_scale && cexp == 1.f && p.row_scale == nullptr && !has_bias;
     // the item's rows of out through a buffer resource: 32-bit offsets, stores past its rows dropped
     const rsrc_t ro = make_rsrc(p.out + row0 * p.ldo, (int64_t)mrows * p.ldo * 2);
+    // SwiGLU fused: act's rows of the item; wave wn's column blocks j = 0, 1 are gate columns
+    // n0 / 2 + 32 wn .. and their up columns, giving act's columns n0 / 2 + 32 wn ..
+    static_assert(!SWI || (kSwiOn && !DB), "the fused SwiGLU pairs blocks j = 0, 1 and takes no fused gradient");
+    constexpr bool swi = SWI;
+    const rsrc_t ra = make_rsrc(swi ? p.act + row0 * p.lda : p.out, swi ? (int64_t)mrows * p.lda * 2 : 0);
+    const int acol = (n0 >> 1) + wn * 32;
+    // a tall item's extra rows: wave (1, wn) holds the up block of wave (0, wn)'s gate block and hands
+    // its values over here ([WAVES_N][64 lanes][8 dwords], past the column-scale and bias tiles)
+    uint32_t* const xch = (uint32_t*)(Lb + BN * LP + BN * 4);
+    (void)xch;
+    (void)acol;
+    static_assert(!TALL || BN * LP + BN * 4 + WAVES_N * 64 * 8 * 2 <= SE, "the tall rows' hand-over fits in its slot");
     // the output blocks: row block i (rows (i * WAVES_M + wm) * 32 ..) x column block j * WAVES_N + wn,
     // and for a tall item one more, i = FM: its extra rows x column block wm * WAVES_N + wn
 #pragma unroll
@@ -1045,6 +1110,7 @@ __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_ker
       const bool tb = TALL && i == FM;
       if (tb ? !tall : i >= am) continue;
       const int rbase = tb ? BM : (i * WAVES_M + wm) * 32;
+      u32x2 pg[4];  // SwiGLU fused: the gate block's values, before the swaps
 #pragma unroll
       for (int j = 0; j < FN; ++j) {
         if (j >= an || (tb && j != wm)) continue;
@@ -1063,9 +1129,7 @@ __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_ker
             }
           }
         }
-        // lane l holds columns 8g + 4(l/32) .. +3 of row l % 32 for g = 0..3; one swap of the lanes'
-        // halves per pair of groups gives lane l < 32 columns 16h .. 16h+7 and lane l + 32 columns
-        // 16h+8 .. 16h+15 (h = 0, 1)
+        // lane l holds columns 8g + 4(l/32) .. +3 of row l % 32 in pk[g], g = 0..3
         u32x2 pk[4];
         if (plain) {  // no stack scale, row scale or bias: one fma per value
 #pragma unroll
@@ -1093,34 +1157,34 @@ __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_ker
             pk[g] = u32x2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
           }
         }
+        if constexpr (swi) {
+          if (j == 0) {
 #pragma unroll
-        for (int h = 0; h < 2; ++h)
+            for (int g = 0; g < 4; ++g) pg[g] = pk[g];
+          } else if (!tb) {
+            u32x2 pa[4];
 #pragma unroll
-          for (int d = 0; d < 2; ++d) {
-            const auto sw = __builtin_amdgcn_permlane32_swap(pk[2 * h][d], pk[2 * h + 1][d], false, false);
-            pk[2 * h][d] = sw[0];
-            pk[2 * h + 1][d] = sw[1];
+            for (int g = 0; g < 4; ++g)
+              pa[g] = u32x2{swiglu_bf16x2(pg[g][0], pk[g][0]), swiglu_bf16x2(pg[g][1], pk[g][1])};
+            store_block32(pa, ra, rbase, p.lda, acol, p.swi, lane);
+          } else {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) *(u32x2*)(xch + (wn * 64 + lane) * 8 + 2 * g) = pk[g];
           }
-        // lane l < 32 now holds columns 0-7 (x) and 16-23 (y) of row l, lane l + 32 columns 8-15 and 24-31;
-        // in 16-lane rows, x = [r0-15 c0-7, r16-31 c0-7, r0-15 c8-15, r16-31 c8-15] and y likewise for
-        // c16-31.  A 32-lane swap then a 16-lane swap regroup them into a = [c0-7, c8-15, c16-23, c24-31] of
-        // rows 0-15 and b the same of rows 16-31: each store then writes 64 contiguous bytes of 16 rows
-        // (rows past the item's are dropped by the output's buffer range)
-        {
-          uint32_t xa[4] = {pk[0][0], pk[0][1], pk[1][0], pk[1][1]}, yb[4] = {pk[2][0], pk[2][1], pk[3][0], pk[3][1]};
+        }
+        store_block32(pk, ro, rbase, p.ldo, tile_col<SWI>(p, n0, (j * WAVES_N + wn) * 32), p.N, lane);
+      }
+      if constexpr (TALL && swi) {
+        if (tb) {  // every wave is here (a tall item): the up blocks handed over, then act
+          __syncthreads();
+          if (wm == 0) {
+            u32x2 pa[4];
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const auto s1 = __builtin_amdgcn_permlane32_swap(xa[q], yb[q], false, false);
-            const auto s2 = __builtin_amdgcn_permlane16_swap(s1[0], s1[1], false, false);
-            xa[q] = s2[0];
-            yb[q] = s2[1];
-          }
-          const int n = n0 + (j * WAVES_N + wn) * 32 + 8 * (lane >> 4);
-          const uint32_t ora = (uint32_t)((rbase + (lane & 15)) * p.ldo * 2) + (uint32_t)n * 2;
-          if (n < p.N) {
-            __builtin_amdgcn_raw_buffer_store_b128(u32x4{xa[0], xa[1], xa[2], xa[3]}, ro, ora, 0, 0);
-            __builtin_amdgcn_raw_buffer_store_b128(u32x4{yb[0], yb[1], yb[2], yb[3]}, ro,
-                                                   ora + (uint32_t)(16 * p.ldo * 2), 0, 0);
+            for (int g = 0; g < 4; ++g) {
+              const u32x2 pu = *(const u32x2*)(xch + (wn * 64 + lane) * 8 + 2 * g);
+              pa[g] = u32x2{swiglu_bf16x2(pg[g][0], pu[0]), swiglu_bf16x2(pg[g][1], pu[1])};
+            }
+            store_block32(pa, ra, rbase, p.lda, acol, p.swi, lane);
           }
         }
       }
@@ -1182,12 +1246,12 @@ __global__ __launch_bounds__(256) void db_finish_kernel(const float* __restrict_
   }
 }
 
-template <bool BKC, int NRB, int WT, bool TALL = false, bool DB = false>
+template <bool BKC, int NRB, int WT, bool TALL = false, bool DB = false, bool SWI = false>
 static int launch_t(const GemmArgs& a, hipStream_t s) {
   if constexpr (kTallOn<BKC, NRB, WT> && !TALL) {
-    if (a.E <= kSmallLastE) return launch_t<BKC, NRB, WT, true, DB>(a, s);
+    if (a.E <= kSmallLastE) return launch_t<BKC, NRB, WT, true, DB, SWI>(a, s);
   }
-  auto kern = grouped_gemm_bf16_kernel<BKC, NRB, WT, TALL, DB>;
+  auto kern = grouped_gemm_bf16_kernel<BKC, NRB, WT, TALL, DB, SWI>;
   const size_t lds = lds_bytes(a.E, WT);
   static std::mutex mu;
   static std::unordered_map<int64_t, int> grid_cache;
@@ -1225,6 +1289,13 @@ static int launch_t(const GemmArgs& a, hipStream_t s) {
 
 template <bool BKC, int WT>
 static int launch_r(const GemmArgs& a, hipStream_t s) {
+  if (a.swi != 0) {  // the fused SwiGLU: forward stacks (bf16, fp8, NF4 either way), rank 16 or no adapters
+    if constexpr (kSwiOn && WT != kWFp8K) {
+      if (a.rank == 0) return launch_t<BKC, 0, WT, false, false, true>(a, s);
+      if (a.rank == 16) return launch_t<BKC, 1, WT, false, false, true>(a, s);
+    }
+    return fail("grouped_gemm_swiglu: the fused SwiGLU takes bf16, fp8 or NF4 stacks with adapters of rank 16 or none");
+  }
   switch (a.rank / 16) {
     case 0: return launch_t<BKC, 0, WT>(a, s);
     case 1: return launch_t<BKC, 1, WT>(a, s);
@@ -1248,6 +1319,7 @@ int launch_grouped_gemm_bf16(const GemmArgs& a, bool k_contiguous, hipStream_t s
 
 int64_t grouped_gemm_db_slots(int64_t rows, int E) { return E + rows / dma::BM + 1; }
 int grouped_gemm_db_max_experts() { return dma::kDbMaxE; }
+bool grouped_gemm_swiglu_fits() { return dma::kSwiOn; }
 
 bool grouped_gemm_dma_takes(const GemmArgs& a, int w_dtype, bool k_contiguous, bool scale_on_k) {
   // fp8 and NF4 stacks: k contiguous (each row copied as stored), rows of whole 16-byte chunks, a

@@ -534,6 +534,90 @@ def test_a_scale_of_the_wrong_shape_is_refused(is_transposed):
     lora_linear(x, stack, scale, offsets, is_transposed, products_fp8=False)  # the right shape is taken
 
 
+@pytest.mark.parametrize("kind", ["bf16", "fp8", "fp8_row", "nf4"])
+@pytest.mark.parametrize("is_transposed", [False, True])
+@pytest.mark.parametrize("rank", [0, 16])
+def test_the_gathered_product_with_swiglu_is_the_product_then_swiglu(kind, is_transposed, rank, monkeypatch):
+    """mlora_grouped_gemm_gather_swiglu: out and low carry the bits of mlora_grouped_gemm_gather_q's, and act
+    those of mlora_swiglu(out), though each tile now holds 128 gate columns and the 128 up columns paired
+    with them (I = 384: three tiles); experts of 1, 257 (tall), 288 (tall, full), 300, 0 and 545 rows and
+    sentinel rows; a bias; bf16, fp8 (per expert, per output row) and NF4 stacks."""
+    from meepsquared_amd import _fp8, _grouped, _lib, _nf4, sort_by_expert
+    from meepsquared_amd._lib import call, ptr
+
+    monkeypatch.setenv("MEEPSQUARED_FUSED_SWIGLU", "1")
+    torch.manual_seed(31 + rank)
+    counts = [1, 257, 288, 300, 0, 545, 40]
+    E, k, K, I = len(counts), 3, 192, 384
+    N = 2 * I
+    ids = torch.repeat_interleave(torch.arange(E + 1), torch.tensor(counts + [3]))  # 3 sentinel rows
+    idx = ids[torch.randperm(ids.numel())].reshape(-1, k).cuda()
+    T = idx.shape[0]
+    perm, inv, offsets = sort_by_expert(idx, E)
+    offsets = offsets.to(torch.int32)
+    h = torch.randn(T, K, device="cuda", dtype=torch.bfloat16)
+    weight = torch.randn((E, K, N) if is_transposed else (E, N, K), device="cuda", dtype=torch.bfloat16) * 0.05
+    scale = None
+    if kind in ("fp8", "fp8_row"):
+        weight, scale = _fp8.quantize_stack(weight, per_row=kind == "fp8_row", is_transposed=is_transposed)
+    elif kind == "nf4":
+        weight = _nf4.quantize_stack(weight)
+    ad = _grouped._Adapters(*adapters(E, K, N, rank, is_transposed), is_transposed) if rank else None
+    bias = torch.randn(E, N, device="cuda", dtype=torch.bfloat16)
+    args = (h, perm, k, weight, scale, offsets, is_transposed, ad, 2.0, bias)
+    out, low, act = _grouped._launch_gathered(*args, swiglu=True)
+    out2, low2 = _grouped._launch_gathered(*args)
+    act2 = torch.empty_like(act)
+    call("mlora_swiglu", ptr(out2), out2.shape[0], I, ptr(act2), _lib.stream())
+    torch.cuda.synchronize()
+    live = int(offsets[-1])
+    assert torch.equal(out[:live], out2[:live])
+    if rank:
+        assert torch.equal(low[:live], low2[:live])
+    assert torch.equal(act[:live], act2[:live])
+    assert act[:live].abs().sum() > 0
+
+
+def test_the_gathered_product_with_swiglu_refuses_what_it_does_not_pair(monkeypatch):
+    """N = 2 I must be a multiple of 256 (each tile pairs 128 gate and 128 up columns), the product a forward
+    one and the adapters of rank 16 or none: the host refuses N = 400 and rank 32, and so does the C entry
+    point."""
+    from meepsquared_amd import _grouped, _lib, sort_by_expert
+    from meepsquared_amd._lib import KernelError, ptr
+
+    E, k, K, N, T = 2, 2, 64, 400, 16
+    idx = torch.randint(0, E, (T, k), device="cuda")
+    perm, inv, offsets = sort_by_expert(idx, E)
+    offsets = offsets.to(torch.int32)
+    h = torch.randn(T, K, device="cuda", dtype=torch.bfloat16)
+    w = torch.randn(E, N, K, device="cuda", dtype=torch.bfloat16)
+    monkeypatch.delenv("MEEPSQUARED_FUSED_SWIGLU", raising=False)
+    assert not _grouped.swiglu_fusable(512)  # off unless asked for
+    monkeypatch.setenv("MEEPSQUARED_FUSED_SWIGLU", "1")
+    assert not _grouped.swiglu_fusable(N) and _grouped.swiglu_fusable(512) and _grouped.swiglu_fusable(512, 16)
+    assert not _grouped.swiglu_fusable(512, backward=True) and not _grouped.swiglu_fusable(512, 32)
+    with pytest.raises(ValueError, match="N % 256"):
+        _grouped._launch_gathered(h, perm, k, w, None, offsets, False, None, 1.0, None, swiglu=True)
+    out = torch.empty(T * k, N, device="cuda", dtype=torch.bfloat16)
+    act = torch.empty(T * k, N // 2, device="cuda", dtype=torch.bfloat16)
+    with pytest.raises(KernelError, match="multiple of 256"):
+        _lib.call("mlora_grouped_gemm_gather_swiglu", ptr(h), K, T, ptr(perm), k, T * k, K, N, ptr(w), _lib.dtype_code(w.dtype),
+                  w.stride(0), w.stride(2), w.stride(1), None, 0, 0, None, None, None, None, None,
+                  None, 0, 0, None, 0, 0, 0, 1.0, None, 0, ptr(out), N, None, 0, ptr(act), N // 2,
+                  ptr(offsets), E, _lib.stream())
+    N = 512  # pairs, but rank 32 is not taken
+    w = torch.randn(E, N, K, device="cuda", dtype=torch.bfloat16)
+    at = torch.randn(E, 32, K, device="cuda", dtype=torch.bfloat16)
+    bt = torch.randn(E, N, 32, device="cuda", dtype=torch.bfloat16)
+    out = torch.empty(T * k, N, device="cuda", dtype=torch.bfloat16)
+    act = torch.empty(T * k, N // 2, device="cuda", dtype=torch.bfloat16)
+    with pytest.raises(KernelError, match="rank 16 or none"):
+        _lib.call("mlora_grouped_gemm_gather_swiglu", ptr(h), K, T, ptr(perm), k, T * k, K, N, ptr(w),
+                  _lib.dtype_code(w.dtype), w.stride(0), w.stride(2), w.stride(1), None, 0, 0, None, None, None, None,
+                  None, ptr(at), at.stride(0), at.stride(1), ptr(bt), bt.stride(0), bt.stride(1), 32, 1.0, None, 0,
+                  ptr(out), N, None, 0, ptr(act), N // 2, ptr(offsets), E, _lib.stream())
+
+
 def test_the_gathered_products_refuse_what_their_kernel_does_not_take():
     """The gathered product reads bf16, fp8 and NF4 stacks whose rows are whole 16-byte chunks (NF4: 64-code
     blocks) and applies a per-row stack scale along k only in the fp8 decode: an fp8 stack with rows of 72

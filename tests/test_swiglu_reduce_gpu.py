@@ -95,8 +95,9 @@ def test_the_fused_swiglu_backward_matches_the_kernels_it_replaces(case, w_dtype
 
 def test_the_layer_takes_the_fused_swiglu_backward_and_matches_the_two_reductions(monkeypatch):
     """The routed layer with both adapters at rank 16: the gate_up backward takes the B gradient the SwiGLU
-    backward formed (one grouped_reduce launch fewer per projection), with the same gradients as the layer
-    run without the link between its two Functions."""
+    backward formed (one grouped_reduce launch fewer per projection) and the down Function the SwiGLU the
+    gate_up product formed (no SwiGLU pass, with MEEPSQUARED_FUSED_SWIGLU=1), with the same output and
+    gradients as the layer run without the link between its two Functions."""
     from meepsquared_amd import Experts, _grouped, routed_forward, topk_softmax
 
     torch.manual_seed(5)
@@ -112,10 +113,20 @@ def test_the_layer_takes_the_fused_swiglu_backward_and_matches_the_two_reduction
                        (torch.randn(E, r, I, device=dev) * 0.1).bfloat16(), 2.0)}
     dy = torch.randn(T, H, device=dev).bfloat16()
     counts = {}
+    monkeypatch.setenv("MEEPSQUARED_FUSED_SWIGLU", "1")
 
     def observe(kind, phase, info):
         if phase == "before":
             counts[kind] = counts.get(kind, 0) + 1
+
+    real_call = _grouped.call
+
+    def call(name, *args):  # counts the standalone SwiGLU launches
+        if name == "mlora_swiglu":
+            counts[name] = counts.get(name, 0) + 1
+        return real_call(name, *args)
+
+    monkeypatch.setattr(_grouped, "call", call)
 
     def run(linked):
         hh = h.clone().requires_grad_()
@@ -123,7 +134,7 @@ def test_the_layer_takes_the_fused_swiglu_backward_and_matches_the_two_reduction
         w, idx = topk_softmax(logits, k)
         w = w.detach().requires_grad_()
         if not linked:
-            monkeypatch.setattr(_grouped, "GateUpLink", lambda: None)
+            monkeypatch.setattr(_grouped, "GateUpLink", lambda **kw: None)
         counts.clear()
         monkeypatch.setattr(_grouped, "launch_observer", observe)
         out = routed_forward(Experts(gu, dn), hh, idx, w, ff)
@@ -138,6 +149,8 @@ def test_the_layer_takes_the_fused_swiglu_backward_and_matches_the_two_reduction
     for i, (a, b) in enumerate(zip(got, want)):
         assert rel(a.float(), b.float()) < 1e-2, i
     assert got_counts.get("grouped_reduce", 0) == want_counts.get("grouped_reduce", 0) - 2, (got_counts, want_counts)
+    # and SwiGLU formed in the gate_up product's epilogue: the same bits (out above), no SwiGLU pass
+    assert got_counts.get("mlora_swiglu", 0) == 0 and want_counts.get("mlora_swiglu", 0) == 1, (got_counts, want_counts)
 
 
 def _bf16_ulp(v):
