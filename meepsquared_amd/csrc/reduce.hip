@@ -412,7 +412,7 @@ __global__ __launch_bounds__(256) void swiglu_backward_reduce_kernel(
         }
         // the row's 64 columns: the eight lanes that hold it, summed in a fixed order
         dot = sum8(live ? dot : 0.f);
-        if ((lane & 7) == 0 && rr < nb) dwp[(b0 + rr) * nblk + nbk] = dot;
+        if ((lane & 7) == 0 && rr < nb) dwp[nbk * rows + b0 + rr] = dot;  // [strip][row]: a chunk's 32 rows contiguous
       }
       const bool lrow = r0 + lr < nb;
       u32x4 la = ch.a, lb = ch.b;
@@ -508,7 +508,7 @@ __global__ __launch_bounds__(256) void swiglu_reduce_rows_kernel(const float* __
   for (int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; r < rows; r += (int64_t)gridDim.x * blockDim.x) {
     float s = 0.f;
     if (r < valid) {
-      for (int c = 0; c < nblk; ++c) s += dwp[r * nblk + c];
+      for (int c = 0; c < nblk; ++c) s += dwp[c * rows + r];
     } else {
       for (int64_t c = 0; c < I2; c += 8) *(u32x4*)(dgu + r * I2 + c) = u32x4{0u, 0u, 0u, 0u};
     }
@@ -620,7 +620,7 @@ extern "C" int mlora_grouped_reduce_gather(const void* g, int64_t ldg, const int
                              offsets, E, out, o_se, o_sn, o_sr, workspace, workspace_bytes, stream);
 }
 
-// dw parts [rows][I / 64] fp32 (256-byte aligned), then, when an expert can be split, the parts' sums
+// dw parts [I / 64][rows] fp32 (256-byte aligned), then, when an expert can be split, the parts' sums
 static size_t swiglu_reduce_dw_bytes(int64_t S, int64_t I) {
   const int64_t nblk = (I + RB_N - 1) / RB_N;
   return (size_t)((S * nblk * (int64_t)sizeof(float) + 255) & ~(int64_t)255);
