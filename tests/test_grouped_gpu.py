@@ -578,6 +578,43 @@ def test_the_gathered_product_with_swiglu_is_the_product_then_swiglu(kind, is_tr
     assert act[:live].abs().sum() > 0
 
 
+@pytest.mark.parametrize("rank", [0, 16])
+def test_the_gathered_product_with_swiglu_over_more_experts_than_take_tall_items(rank, monkeypatch):
+    """With more than 1024 experts the product runs without tall items (the launch's other instantiation):
+    1100 experts, a few holding 257-300 rows (a full tile and a small one), the rest 0-40 rows; out, low and
+    act as in the product then mlora_swiglu, to the bit."""
+    from meepsquared_amd import _grouped, _lib, sort_by_expert
+    from meepsquared_amd._lib import call, ptr
+
+    monkeypatch.setenv("MEEPSQUARED_FUSED_SWIGLU", "1")
+    torch.manual_seed(41 + rank)
+    E, k, K, I = 1100, 2, 128, 128
+    N = 2 * I
+    counts = torch.randint(0, 41, (E,))
+    counts[[3, 500, 1099]] = torch.tensor([257, 300, 290])
+    total = int(counts.sum())
+    pad = (-total) % k
+    ids = torch.repeat_interleave(torch.arange(E + 1), torch.cat([counts, torch.tensor([pad])]))
+    idx = ids[torch.randperm(ids.numel())].reshape(-1, k).cuda()
+    T = idx.shape[0]
+    perm, inv, offsets = sort_by_expert(idx, E)
+    offsets = offsets.to(torch.int32)
+    h = torch.randn(T, K, device="cuda", dtype=torch.bfloat16)
+    weight = torch.randn(E, N, K, device="cuda", dtype=torch.bfloat16) * 0.05
+    ad = _grouped._Adapters(*adapters(E, K, N, rank, False), False) if rank else None
+    args = (h, perm, k, weight, None, offsets, False, ad, 2.0, None)
+    out, low, act = _grouped._launch_gathered(*args, swiglu=True)
+    out2, low2 = _grouped._launch_gathered(*args)
+    act2 = torch.empty_like(act)
+    call("mlora_swiglu", ptr(out2), out2.shape[0], I, ptr(act2), _lib.stream())
+    torch.cuda.synchronize()
+    live = int(offsets[-1])
+    assert torch.equal(out[:live], out2[:live])
+    if rank:
+        assert torch.equal(low[:live], low2[:live])
+    assert torch.equal(act[:live], act2[:live])
+
+
 def test_the_gathered_product_with_swiglu_refuses_what_it_does_not_pair(monkeypatch):
     """N = 2 I must be a multiple of 256 (each tile pairs 128 gate and 128 up columns), the product a forward
     one and the adapters of rank 16 or none: the host refuses N = 400 and rank 32, and so does the C entry
