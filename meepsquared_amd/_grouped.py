@@ -480,8 +480,8 @@ def swiglu_fusable(N, rank=0, row_scale=None, backward=False) -> bool:
     """Whether the gathered product of a gate_up stack (N = 2 I columns) forms SwiGLU in its epilogue
     (mlora_grouped_gemm_gather_swiglu): asked for with MEEPSQUARED_FUSED_SWIGLU=1, and a forward product
     without row scale, N a multiple of 256, adapters padded to rank 16 or none.  Off by default: on MI355X at
-    the Qwen3-shaped layer the fused epilogue adds about what the SwiGLU pass it replaces takes (+33 us to the
-    gate_up product against 46 us)."""
+    the Qwen3-shaped layer the fused epilogue adds about what the SwiGLU pass it replaces takes (+30 us to the
+    gate_up product against 46 us; the step within 0.3 %)."""
     return (os.environ.get("MEEPSQUARED_FUSED_SWIGLU", "0") == "1" and not backward and row_scale is None
             and N % 256 == 0 and N > 0 and rank in (0, 16))
 
