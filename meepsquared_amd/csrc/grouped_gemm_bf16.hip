@@ -118,7 +118,10 @@ __device__ __forceinline__ void stage_barrier() {
 }
 
 // The tile map in LDS, one int per expert: tend[e] = the number of BM-row tiles of experts 0..e
-// (an inclusive scan; tend[E-1] is the tile count).  Expert e's rows are [start(e), start(e+1)) with
+// (an inclusive scan; tend[E-1] is the tile count).  With tall items an expert's remainder of at most XR
+// rows past its full tiles joins its last tile (BM + XR rows at most); with tall2, a remainder of XR + 1 ..
+// 2 XR rows past at least two full tiles is spread over the last two (the first takes rem - XR extra rows,
+// the last XR), so that no near-empty tile of its own is left for the launch's last round.  Expert e's rows are [start(e), start(e+1)) with
 // start(e) = offsets[e-1] clamped into [0, rows] (start(0) = 0), read from global memory when needed.
 // With small_last, an expert's last tile when it holds at most BM/2 rows is counted apart, in sfx[e]
 // (0 or 1, scanned the same way): those tiles are scheduled after all the others, so that they fill
@@ -146,12 +149,13 @@ __device__ __forceinline__ void scan_wave(int* v, int E, int lane) {  // inclusi
 }
 
 __device__ __forceinline__ void build_tile_ends(const GemmArgs& p, int* tend, int* sfx, bool small_last, bool tall,
-                                                int tid) {
+                                                bool tall2, int tid) {
   const int E = p.E;
   for (int e = tid; e < E; e += kThreads) {
     const int64_t c = row_start(p, e + 1) - row_start(p, e);
     int nt = c > 0 ? (int)((c + BM - 1) / BM) : 0;
     if (tall && nt >= 2 && c - (int64_t)(nt - 1) * BM <= XR) --nt;  // the remainder joins the last full tile
+    else if (tall2 && nt >= 3 && c - (int64_t)(nt - 1) * BM <= 2 * XR) --nt;  // ... or the last two
     const int small = small_last && nt > 0 && c - (int64_t)(nt - 1) * BM <= BM / 2;
     tend[e] = nt - small;
     if (small_last) sfx[e] = small;
@@ -174,7 +178,7 @@ __device__ __forceinline__ int first_above(const int* v, int E, int t) {  // the
 // work item (tile t, column block) -> wave-uniform expert, rows and columns; small: t counts the
 // small last tiles
 __device__ __forceinline__ Item decode(const GemmArgs& p, int64_t item, int nb, const int* tend, const int* sfx,
-                                       bool small, bool tall) {
+                                       bool small, bool tall, bool tall2) {
   const int t = (int)(item / nb);
   Item it;
   it.nblk = (int)(item - (int64_t)t * nb);
@@ -191,6 +195,19 @@ __device__ __forceinline__ Item decode(const GemmArgs& p, int64_t item, int nb, 
   // an item left with at most BM + XR rows is the expert's last (a tall one when it has more than BM)
   const int64_t left = row_start(p, it.e + 1) - it.row0;
   it.mrows = (int)(left <= BM + (tall ? XR : 0) ? left : (int64_t)BM);
+  if (tall2 && !small) {  // the expert's remainder spread over its last two tiles (as build_tile_ends counts)
+    const int t0 = it.e == 0 ? 0 : __builtin_amdgcn_readfirstlane(tend[it.e - 1]);
+    const int nt = __builtin_amdgcn_readfirstlane(tend[it.e]) - t0, j = (int)((it.row0 - row_start(p, it.e)) / BM);
+    const int64_t rem = row_start(p, it.e + 1) - row_start(p, it.e) - (int64_t)nt * BM;
+    if (nt >= 2 && rem > XR && rem <= 2 * XR) {
+      if (j == nt - 2) {
+        it.mrows = BM + (int)(rem - XR);
+      } else if (j == nt - 1) {
+        it.row0 += rem - XR;
+        it.mrows = BM + XR;
+      }
+    }
+  }
   it.n0 = it.nblk * BN;
   return it;
 }
@@ -897,7 +914,7 @@ __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_ker
   if constexpr (WT == kWNf4T) {
     for (int c = tid0; c < 16; c += kThreads) code[c] = p.nf4_code[c];
   }
-  build_tile_ends(p, tile_map, sfx, small_last, TALL, tid0);
+  build_tile_ends(p, tile_map, sfx, small_last, TALL, TALL && !DB, tid0);
   const int nb = (p.N + BN - 1) / BN;
   // each XCD takes one contiguous eighth of the full tiles' items, then one eighth of the small tiles'
   const int64_t nbig = (int64_t)__builtin_amdgcn_readfirstlane(tile_map[E - 1]) * nb;
@@ -916,7 +933,7 @@ __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_ker
     int tid = tid0;
     asm volatile("" : "+v"(tid));
     const int lane = tid & 63;
-    const Item it = decode(p, item, nb, tile_map, sfx, small, TALL);
+    const Item it = decode(p, item, nb, tile_map, sfx, small, TALL, TALL && !DB);
     const int e = it.e, n0 = it.n0, mrows = it.mrows;
     const int64_t row0 = it.row0;
     const int ncols = min(BN, p.N - n0);

@@ -124,11 +124,13 @@ def test_the_product_with_adapters_and_its_gradients_match_pytorch(is_transposed
 
 @pytest.mark.parametrize("is_transposed", [False, True])
 def test_tall_items_match_one_product_per_expert(is_transposed):
-    """Groups whose last tile holds at most 32 rows past a full one (257, 288, 513, 544 rows) are run
-    as one item of up to 288 rows; 289 and 545 rows keep a tile of their own.  Output, input gradient
-    and both adapter gradients against the oracle, with a bias and a column block cut short (N = 320)."""
+    """Groups whose last tile holds at most 32 rows past a full one (257, 288, 513, 544, 800 rows) are run
+    as one item of up to 288 rows; 33-64 rows past at least two full tiles (545, 560, 576, 801, 832 rows)
+    spread over the last two, each of up to 288 rows; 289, 577 and 833 rows keep a tile of their own.
+    Output, input gradient and both adapter gradients against the oracle, with a bias and a column block
+    cut short (N = 320)."""
     torch.manual_seed(0)
-    rows_per_expert = [257, 288, 289, 0, 545, 544, 513, 256, 1, 800, 33, 290]
+    rows_per_expert = [257, 288, 289, 0, 545, 544, 513, 256, 1, 800, 33, 290, 560, 576, 577, 801, 832, 833]
     K, N, rank = 160, 320, 16
     experts = len(rows_per_expert)
     offsets = offsets_of(rows_per_expert)
@@ -151,11 +153,12 @@ def test_tall_items_match_one_product_per_expert(is_transposed):
 @pytest.mark.parametrize("seed", range(6))
 def test_random_groups_around_the_tile_boundaries_match_the_oracle(seed):
     """Seeded sweep: group sizes drawn around every tile boundary (0, 1, 31-33, 255-257, 287-289, 511-513,
-    543-545 rows), random K and N (multiples of 8), both stack layouts, rank 0 / 8 / 16 / 32, with or
-    without a bias; output and all gradients against the oracle."""
+    543-545, 575-577, 831-833 rows), random K and N (multiples of 8), both stack layouts, rank 0 / 8 / 16 /
+    32, with or without a bias; output and all gradients against the oracle."""
     g = torch.Generator().manual_seed(100 + seed)
     pick = lambda xs: xs[int(torch.randint(len(xs), (1,), generator=g))]
-    sizes = [0, 1, 31, 32, 33, 255, 256, 257, 287, 288, 289, 511, 512, 513, 543, 544, 545, 600]
+    sizes = [0, 1, 31, 32, 33, 255, 256, 257, 287, 288, 289, 511, 512, 513, 543, 544, 545, 575, 576, 577, 600, 831,
+             832, 833]
     experts = int(torch.randint(2, 9, (1,), generator=g))
     rows_per_expert = [pick(sizes) for _ in range(experts)]
     K, N = 8 * int(torch.randint(4, 40, (1,), generator=g)), 8 * int(torch.randint(4, 72, (1,), generator=g))
