@@ -1224,12 +1224,14 @@ static_assert(STAGES * SlotSize<1>::kElems * 2 + BN * 16 * 2 + 4096 * 4 <= 16384
               "with one rank block: the slots, the B^T tile and the largest tile map fit in LDS");
 static_assert(WTile<kWNf4>::RowBytes * 2 == 64, "an NF4 stage is one block of 64 codes per row");
 
-// tall items: bf16 stacks, rank 16 or none, two-slot ring, and a tile map small enough to sit beside the
-// larger slots (the small-tile counts included)
-static_assert(STAGES * SlotSize<1, kWBf16, true>::kElems * 2 + BN * 16 * 2 + kSmallLastE * 8 <= 163840,
+// tall items: bf16 and fp8 stacks, rank 16 or none, two-slot ring, and a tile map small enough to sit beside
+// the larger slots (the small-tile counts included)
+static_assert(STAGES * SlotSize<1, kWBf16, true>::kElems * 2 + BN * 16 * 2 + kSmallLastE * 8 <= 163840 &&
+                  STAGES * SlotSize<1, kWFp8K, true>::kElems * 2 + BN * 16 * 2 + kSmallLastE * 8 <= 163840,
               "tall items: the slots, the B^T tile and the tile map fit in LDS");
 template <bool BKC, int NRB, int WT>
-constexpr bool kTallOn = STAGES == 2 && WT == kWBf16 && NRB <= 1 && WAVES_M == 2 && WAVES_N >= 2 && FN == 2;
+constexpr bool kTallOn = STAGES == 2 && (WT == kWBf16 || WT == kWFp8 || WT == kWFp8K) && NRB <= 1 && WAVES_M == 2 &&
+                         WAVES_N >= 2 && FN == 2;  // (NF4 stacks: the tall block's registers spill its K loop)
 
 // The fused adapter gradient: at most kDbMaxE experts, so that the slots, the B^T tile, l's tile and the
 // tile map fit in LDS together
