@@ -507,8 +507,17 @@ __global__ __launch_bounds__(256) void swiglu_reduce_rows_kernel(const float* __
   const int64_t valid = expert_start(offsets, rows, E);
   for (int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; r < rows; r += (int64_t)gridDim.x * blockDim.x) {
     float s = 0.f;
-    if (r < valid) {
-      for (int c = 0; c < nblk; ++c) s += dwp[c * rows + r];
+    if (r < valid) {  // four parts' loads in flight at a time (the strips lie rows apart), added in order
+      int c = 0;
+      for (; c + 4 <= nblk; c += 4) {
+        const float v0 = dwp[c * rows + r], v1 = dwp[(c + 1) * rows + r], v2 = dwp[(c + 2) * rows + r],
+                    v3 = dwp[(c + 3) * rows + r];
+        s += v0;
+        s += v1;
+        s += v2;
+        s += v3;
+      }
+      for (; c < nblk; ++c) s += dwp[c * rows + r];
     } else {
       for (int64_t c = 0; c < I2; c += 8) *(u32x4*)(dgu + r * I2 + c) = u32x4{0u, 0u, 0u, 0u};
     }
