@@ -390,7 +390,7 @@ __global__ __launch_bounds__(256) void swiglu_backward_reduce_kernel(
       ch.a = *(const u32x4*)(l2 + r * ld2 + lc);
       ch.b = *(const u32x4*)(lu + r * ldu + lc);
     };
-    auto consume = [&](Chunk& ch, int c) {
+    auto consume = [&](Chunk& ch, int c, auto&& next) {
       const int r0 = rel0(c);
       u32x4 act[4], dgv[4], duv[4];
 #pragma unroll
@@ -449,22 +449,18 @@ __global__ __launch_bounds__(256) void swiglu_backward_reduce_kernel(
         }
         asm volatile("" ::: "memory");
       };
+      next();  // the next chunk's loads, into the registers this chunk no longer needs
       product(act, l2s, acc_a);
       product(dgv, lus, acc_g);
       product(duv, lus, acc_u);
     };
 
-    // loads two chunks ahead of use, every iteration running both halves (as grouped_reduce_kernel); the
-    // compiler is left to interleave the phases (measured faster here than keeping them in order)
-    Chunk ca, cb_;
+    // one chunk in registers: the next chunk's loads go out once this one's SwiGLU math is done, and run
+    // under its transposes and reduction MFMAs (139 VGPRs, so three waves per SIMD; two chunks in flight
+    // held 203 and ran 7-10 % slower)
+    Chunk ca;
     load(ca, 0);
-    load(cb_, 1);
-    for (int c = 0; c < nc; c += 2) {
-      consume(ca, c);
-      load(ca, c + 2);
-      consume(cb_, c + 1);
-      load(cb_, c + 3);
-    }
+    for (int c = 0; c < nc; ++c) consume(ca, c, [&]() { load(ca, c + 1); });
   }
 
   // the waves' partial sums, added in wave order; acc[cb][v] is column cb*16 + 4*(lane/16) + v, rank lane%16
