@@ -488,6 +488,37 @@ def test_the_input_gradient_through_an_fp8_stack_is_bit_identical_to_its_decoded
 
 
 @pytest.mark.parametrize("is_transposed", [False, True])
+def test_tall_items_of_an_fp8_stack_are_those_of_its_decoded_twin(is_transposed):
+    """fp8 stacks take tall items too (a last tile of up to 288 rows, or a 33-64-row remainder spread over
+    the last two tiles): with one scale per output row and bf16 products, the output and the input gradient
+    over groups at every tile boundary are those of the scaled bf16 twin, to the bit (the forward applies the
+    row scale in the epilogue, so its check is to the oracle's bound instead)."""
+    from meepsquared_amd import _fp8, lora_linear
+
+    torch.manual_seed(13)
+    rows_per_expert = [257, 288, 289, 545, 544, 560, 576, 577, 801, 832, 833, 40]
+    E, K, N, r = len(rows_per_expert), 192, 320, 16
+    offsets = offsets_of(rows_per_expert)
+    w = (torch.randn((E, K, N) if is_transposed else (E, N, K), device="cuda") * 0.05).bfloat16()
+    stack, scale = _fp8.quantize_stack(w, per_row=True, is_transposed=is_transposed)
+    twin = (stack.float() * (scale[:, None, :] if is_transposed else scale[:, :, None])).bfloat16()
+    if is_transposed:
+        lhs, rhs = torch.randn(E, K, r, device="cuda") * 0.1, torch.randn(E, r, N, device="cuda") * 0.1
+    else:
+        lhs, rhs = torch.randn(E, N, r, device="cuda") * 0.1, torch.randn(E, r, K, device="cuda") * 0.1
+    x = torch.randn(sum(rows_per_expert), K, device="cuda").bfloat16()
+    dy = torch.randn(sum(rows_per_expert), N, device="cuda").bfloat16()
+    res = []
+    for wt, sc in ((stack, scale), (twin, None)):
+        xx = x.clone().requires_grad_()
+        out = lora_linear(xx, wt, sc, offsets, is_transposed, lhs.bfloat16(), rhs.bfloat16(), 2.0, products_fp8=False)
+        out.backward(dy)
+        res.append((out.detach(), xx.grad))
+    assert torch.equal(res[0][1], res[1][1])
+    assert rel(res[0][0], res[1][0]) < BF16_TOL
+
+
+@pytest.mark.parametrize("is_transposed", [False, True])
 def test_an_nf4_stack_read_the_other_way_is_bit_identical_to_its_decoded_twin(is_transposed):
     """The product that reads an NF4 stack with its blocks along n (the input gradient of a stack, or
     the forward of a transposed one) goes through the stack's transposed codes and absmax table: each
