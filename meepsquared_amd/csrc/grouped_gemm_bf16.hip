@@ -119,9 +119,11 @@ __device__ __forceinline__ void stage_barrier() {
 
 // The tile map in LDS, one int per expert: tend[e] = the number of BM-row tiles of experts 0..e
 // (an inclusive scan; tend[E-1] is the tile count).  With tall items an expert's remainder of at most XR
-// rows past its full tiles joins its last tile (BM + XR rows at most); with tall2, a remainder of XR + 1 ..
-// 2 XR rows past at least two full tiles is spread over the last two (the first takes rem - XR extra rows,
-// the last XR), so that no near-empty tile of its own is left for the launch's last round.  Expert e's rows are [start(e), start(e+1)) with
+// rows past its full tiles joins its last tile (BM + XR rows at most); with tall2, a larger remainder of at
+// most n XR rows past n >= 2 full tiles is spread over the last m = ceil(rem / XR) of them (the first of those
+// takes rem - (m - 1) XR extra rows, the others XR each), so that no partial tile of its own is left: a tall
+// item costs a few % more than a full one, a partial tile most of one, and near-empty ones fill the launch's
+// last round.  Expert e's rows are [start(e), start(e+1)) with
 // start(e) = offsets[e-1] clamped into [0, rows] (start(0) = 0), read from global memory when needed.
 // With small_last, an expert's last tile when it holds at most BM/2 rows is counted apart, in sfx[e]
 // (0 or 1, scanned the same way): those tiles are scheduled after all the others, so that they fill
@@ -155,7 +157,7 @@ __device__ __forceinline__ void build_tile_ends(const GemmArgs& p, int* tend, in
     const int64_t c = row_start(p, e + 1) - row_start(p, e);
     int nt = c > 0 ? (int)((c + BM - 1) / BM) : 0;
     if (tall && nt >= 2 && c - (int64_t)(nt - 1) * BM <= XR) --nt;  // the remainder joins the last full tile
-    else if (tall2 && nt >= 3 && c - (int64_t)(nt - 1) * BM <= 2 * XR) --nt;  // ... or the last two
+    else if (tall2 && nt >= 3 && c - (int64_t)(nt - 1) * BM <= (int64_t)(nt - 1) * XR) --nt;  // ... or the last m
     const int small = small_last && nt > 0 && c - (int64_t)(nt - 1) * BM <= BM / 2;
     tend[e] = nt - small;
     if (small_last) sfx[e] = small;
@@ -195,16 +197,15 @@ __device__ __forceinline__ Item decode(const GemmArgs& p, int64_t item, int nb, 
   // an item left with at most BM + XR rows is the expert's last (a tall one when it has more than BM)
   const int64_t left = row_start(p, it.e + 1) - it.row0;
   it.mrows = (int)(left <= BM + (tall ? XR : 0) ? left : (int64_t)BM);
-  if (tall2 && !small) {  // the expert's remainder spread over its last two tiles (as build_tile_ends counts)
+  if (tall2 && !small) {  // the expert's remainder spread over its last m tiles (as build_tile_ends counts)
     const int t0 = it.e == 0 ? 0 : __builtin_amdgcn_readfirstlane(tend[it.e - 1]);
     const int nt = __builtin_amdgcn_readfirstlane(tend[it.e]) - t0, j = (int)((it.row0 - row_start(p, it.e)) / BM);
     const int64_t rem = row_start(p, it.e + 1) - row_start(p, it.e) - (int64_t)nt * BM;
-    if (nt >= 2 && rem > XR && rem <= 2 * XR) {
-      if (j == nt - 2) {
-        it.mrows = BM + (int)(rem - XR);
-      } else if (j == nt - 1) {
-        it.row0 += rem - XR;
-        it.mrows = BM + XR;
+    if (nt >= 2 && rem > XR && rem <= (int64_t)nt * XR) {
+      const int m = (int)((rem + XR - 1) / XR), first = nt - m, a = (int)(rem - (int64_t)(m - 1) * XR);
+      if (j >= first) {
+        it.row0 += j == first ? 0 : a + (j - first - 1) * XR;
+        it.mrows = BM + (j == first ? a : XR);
       }
     }
   }

@@ -124,13 +124,14 @@ def test_the_product_with_adapters_and_its_gradients_match_pytorch(is_transposed
 
 @pytest.mark.parametrize("is_transposed", [False, True])
 def test_tall_items_match_one_product_per_expert(is_transposed):
-    """Groups whose last tile holds at most 32 rows past a full one (257, 288, 513, 544, 800 rows) are run
-    as one item of up to 288 rows; 33-64 rows past at least two full tiles (545, 560, 576, 801, 832 rows)
-    spread over the last two, each of up to 288 rows; 289, 577 and 833 rows keep a tile of their own.
-    Output, input gradient and both adapter gradients against the oracle, with a bias and a column block
-    cut short (N = 320)."""
+    """Groups whose last tile holds at most 32 rows past a full one (257, 288, 513, 544, 800, 1300 rows) are
+    run as one item of up to 288 rows; a remainder of at most 32 n rows past n >= 2 full tiles (545, 560, 576,
+    801, 832, 864, 1100, 2000, 2100 rows) is spread over the last ceil(rem / 32) tiles, each of up to 288 rows;
+    289, 577, 865 and 1535 rows keep a tile of their own.  Output, input gradient and both adapter gradients
+    against the oracle, with a bias and a column block cut short (N = 320)."""
     torch.manual_seed(0)
-    rows_per_expert = [257, 288, 289, 0, 545, 544, 513, 256, 1, 800, 33, 290, 560, 576, 577, 801, 832, 833]
+    rows_per_expert = [257, 288, 289, 0, 545, 544, 513, 256, 1, 800, 33, 290, 560, 576, 577, 801, 832, 833, 864,
+                       865, 1100, 1300, 1535, 2000, 2100]
     K, N, rank = 160, 320, 16
     experts = len(rows_per_expert)
     offsets = offsets_of(rows_per_expert)
@@ -489,14 +490,14 @@ def test_the_input_gradient_through_an_fp8_stack_is_bit_identical_to_its_decoded
 
 @pytest.mark.parametrize("is_transposed", [False, True])
 def test_tall_items_of_an_fp8_stack_are_those_of_its_decoded_twin(is_transposed):
-    """fp8 stacks take tall items too (a last tile of up to 288 rows, or a 33-64-row remainder spread over
-    the last two tiles): with one scale per output row and bf16 products, the output and the input gradient
+    """fp8 stacks take tall items too (a last tile of up to 288 rows, or a larger remainder spread over the
+    last tiles, each of up to 288 rows): with one scale per output row and bf16 products, the output and the input gradient
     over groups at every tile boundary are those of the scaled bf16 twin, to the bit (the forward applies the
     row scale in the epilogue, so its check is to the oracle's bound instead)."""
     from meepsquared_amd import _fp8, lora_linear
 
     torch.manual_seed(13)
-    rows_per_expert = [257, 288, 289, 545, 544, 560, 576, 577, 801, 832, 833, 40]
+    rows_per_expert = [257, 288, 289, 545, 544, 560, 576, 577, 801, 832, 833, 40, 1100, 2000]
     E, K, N, r = len(rows_per_expert), 192, 320, 16
     offsets = offsets_of(rows_per_expert)
     w = (torch.randn((E, K, N) if is_transposed else (E, N, K), device="cuda") * 0.05).bfloat16()
