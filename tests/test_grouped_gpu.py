@@ -520,15 +520,18 @@ def test_tall_items_of_an_fp8_stack_are_those_of_its_decoded_twin(is_transposed)
 
 
 @pytest.mark.parametrize("is_transposed", [False, True])
-def test_an_nf4_stack_read_the_other_way_is_bit_identical_to_its_decoded_twin(is_transposed):
+@pytest.mark.parametrize("rows_per_expert", [[100, 0, 300, 37],
+                                             [257, 288, 289, 545, 544, 560, 576, 577, 801, 832, 833, 40, 1100, 2000]])
+def test_an_nf4_stack_read_the_other_way_is_bit_identical_to_its_decoded_twin(is_transposed, rows_per_expert):
     """The product that reads an NF4 stack with its blocks along n (the input gradient of a stack, or
     the forward of a transposed one) goes through the stack's transposed codes and absmax table: each
     value decodes as bf16(code · absmax) with the absmax of its own block, so the input gradient (and,
-    for a transposed stack, the output) is that of the decoded bf16 twin, to the bit."""
+    for a transposed stack, the output) is that of the decoded bf16 twin, to the bit; the second group
+    list puts a group at every tile boundary (the sizes bf16 and fp8 stacks take as tall items; NF4
+    stacks run them as full tiles plus a partial one)."""
     from meepsquared_amd import _nf4, lora_linear
 
     torch.manual_seed(8)
-    rows_per_expert = [100, 0, 300, 37]
     E, K, N, r = len(rows_per_expert), 256, 320, 16
     offsets = offsets_of(rows_per_expert)
     w = torch.randn((E, K, N) if is_transposed else (E, N, K), device="cuda") * 0.05
