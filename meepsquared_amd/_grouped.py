@@ -478,11 +478,11 @@ def gathered_product_fits(weight, products_fp8=None) -> bool:
 
 def swiglu_fusable(N, rank=0, row_scale=None, backward=False) -> bool:
     """Whether the gathered product of a gate_up stack (N = 2 I columns) forms SwiGLU in its epilogue
-    (mlora_grouped_gemm_gather_swiglu): asked for with MEEPSQUARED_FUSED_SWIGLU=1, and a forward product
-    without row scale, N a multiple of 256, adapters padded to rank 16 or none.  Off by default: on MI355X at
-    the Qwen3-shaped layer the fused epilogue adds about what the SwiGLU pass it replaces takes (+30 us to the
-    gate_up product against 46 us; the step within 0.3 %)."""
-    return (os.environ.get("MEEPSQUARED_FUSED_SWIGLU", "0") == "1" and not backward and row_scale is None
+    (mlora_grouped_gemm_gather_swiglu): a forward product without row scale, N a multiple of 256, adapters
+    padded to rank 16 or none, unless MEEPSQUARED_FUSED_SWIGLU=0 asks for the separate SwiGLU pass.  On MI355X
+    the fused epilogue costs less than the pass it replaces (Qwen3-shaped layer: +30 us to the gate_up product
+    against a 46 us pass, the step +0.4 %; Mixtral-shaped: +1 %)."""
+    return (os.environ.get("MEEPSQUARED_FUSED_SWIGLU", "1") != "0" and not backward and row_scale is None
             and N % 256 == 0 and N > 0 and rank in (0, 16))
 
 

@@ -666,9 +666,9 @@ def test_the_gathered_product_with_swiglu_refuses_what_it_does_not_pair(monkeypa
     offsets = offsets.to(torch.int32)
     h = torch.randn(T, K, device="cuda", dtype=torch.bfloat16)
     w = torch.randn(E, N, K, device="cuda", dtype=torch.bfloat16)
-    monkeypatch.delenv("MEEPSQUARED_FUSED_SWIGLU", raising=False)
-    assert not _grouped.swiglu_fusable(512)  # off unless asked for
-    monkeypatch.setenv("MEEPSQUARED_FUSED_SWIGLU", "1")
+    monkeypatch.setenv("MEEPSQUARED_FUSED_SWIGLU", "0")
+    assert not _grouped.swiglu_fusable(512)  # the separate pass, asked for
+    monkeypatch.delenv("MEEPSQUARED_FUSED_SWIGLU", raising=False)  # on by default
     assert not _grouped.swiglu_fusable(N) and _grouped.swiglu_fusable(512) and _grouped.swiglu_fusable(512, 16)
     assert not _grouped.swiglu_fusable(512, backward=True) and not _grouped.swiglu_fusable(512, 32)
     with pytest.raises(ValueError, match="N % 256"):

@@ -96,7 +96,7 @@ def test_the_fused_swiglu_backward_matches_the_kernels_it_replaces(case, w_dtype
 def test_the_layer_takes_the_fused_swiglu_backward_and_matches_the_two_reductions(monkeypatch):
     """The routed layer with both adapters at rank 16: the gate_up backward takes the B gradient the SwiGLU
     backward formed (one grouped_reduce launch fewer per projection) and the down Function the SwiGLU the
-    gate_up product formed (no SwiGLU pass, with MEEPSQUARED_FUSED_SWIGLU=1), with the same output and
+    gate_up product formed (no SwiGLU pass, the default), with the same output and
     gradients as the layer run without the link between its two Functions."""
     from meepsquared_amd import Experts, _grouped, routed_forward, topk_softmax
 
@@ -113,7 +113,7 @@ def test_the_layer_takes_the_fused_swiglu_backward_and_matches_the_two_reduction
                        (torch.randn(E, r, I, device=dev) * 0.1).bfloat16(), 2.0)}
     dy = torch.randn(T, H, device=dev).bfloat16()
     counts = {}
-    monkeypatch.setenv("MEEPSQUARED_FUSED_SWIGLU", "1")
+    monkeypatch.delenv("MEEPSQUARED_FUSED_SWIGLU", raising=False)
 
     def observe(kind, phase, info):
         if phase == "before":
