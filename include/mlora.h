@@ -333,6 +333,16 @@ int mlora_scale_rows(const void* l, int64_t ldl, int64_t rows, int64_t R, const 
 int mlora_swap_adapters(const void* at, int64_t at_se, int64_t at_sr, const void* bt, int64_t bt_se, int64_t bt_sn,
                         int64_t E, int64_t R, int64_t K, int64_t N, void* at_out, void* bt_out, void* stream);
 
+/* mlora_swap_adapters for two projections in one launch (the layer's down and gate_up adapters, swapped at
+ * the first input-gradient product of the backward; _grouped.py:304-310 swaps each projection's factors
+ * when its own backward runs): the first projection's arguments, then the second's, each as
+ * mlora_swap_adapters takes them. */
+int mlora_swap_adapters_two(const void* at, int64_t at_se, int64_t at_sr, const void* bt, int64_t bt_se,
+                            int64_t bt_sn, int64_t E, int64_t R, int64_t K, int64_t N, void* at_out, void* bt_out,
+                            const void* at2, int64_t at2_se, int64_t at2_sr, const void* bt2, int64_t bt2_se,
+                            int64_t bt2_sn, int64_t E2, int64_t R2, int64_t K2, int64_t N2, void* at2_out,
+                            void* bt2_out, void* stream);
+
 /* dst[e][b][a] = src[e*s_e + a*s_a + b*s_b] (bf16): a batched transpose into a contiguous (E, B, A)
  * tensor, for the adapters' roles in the input-gradient product, which
  * src/meepsquared/_grouped.py:304-310 (_Adapters.swapped) addresses by strides. */

@@ -138,20 +138,47 @@ class _Adapters:
         self.at = _padded_rank(at, 1).to(torch.bfloat16).contiguous()  # (e, R, k)
         self.bt = _padded_rank(bt, 2).to(torch.bfloat16).contiguous()  # (e, n, R)
         self.padded = self.at.shape[1]
+        self.partner = None  # another projection's adapters, swapped in the same launch as these
+        self._swapped = None  # these adapters swapped by the partner's launch, not yet taken
 
-    def swapped(self):
-        """The adapters of the input-gradient product: B takes A's role and A B's (_grouped.py:304-310)."""
-        other = object.__new__(_Adapters)
-        other.rank, other.padded = self.rank, self.padded
+    def _pairable(self):
         E, R, K = self.at.shape
         N = self.bt.shape[1]
-        if R in (16, 32) and K > R and N > R and K % 8 == 0 and N % 8 == 0:  # both transposes in one launch
-            other.at = torch.empty((E, R, N), device=self.at.device, dtype=torch.bfloat16)
-            other.bt = torch.empty((E, K, R), device=self.at.device, dtype=torch.bfloat16)
-            call("mlora_swap_adapters", ptr(self.at), self.at.stride(0), self.at.stride(1), ptr(self.bt),
-                 self.bt.stride(0), self.bt.stride(1), E, R, K, N, ptr(other.at), ptr(other.bt),
-                 _lib.stream(self.at.device))
+        return R in (16, 32) and K > R and N > R and K % 8 == 0 and N % 8 == 0
+
+    def _empty_swapped(self):
+        other = object.__new__(_Adapters)
+        other.rank, other.padded, other.partner, other._swapped = self.rank, self.padded, None, None
+        E, R, K = self.at.shape
+        other.at = torch.empty((E, R, self.bt.shape[1]), device=self.at.device, dtype=torch.bfloat16)
+        other.bt = torch.empty((E, K, R), device=self.at.device, dtype=torch.bfloat16)
+        return other
+
+    def _swap_args(self, other):
+        E, R, K = self.at.shape
+        return (ptr(self.at), self.at.stride(0), self.at.stride(1), ptr(self.bt), self.bt.stride(0), self.bt.stride(1),
+                E, R, K, self.bt.shape[1], ptr(other.at), ptr(other.bt))
+
+    def swapped(self):
+        """The adapters of the input-gradient product: B takes A's role and A B's (_grouped.py:304-310).  With
+        a partner (the layer's other projection) whose swap is still to come, both are swapped in one launch
+        and the partner keeps its result until its own backward takes it (once)."""
+        if self._swapped is not None:
+            other, self._swapped = self._swapped, None
+            return other
+        if self._pairable():  # both transposes in one launch
+            other = self._empty_swapped()
+            p = self.partner
+            if (p is not None and p._swapped is None and p._pairable() and p.at.device == self.at.device):
+                p_other = p._empty_swapped()
+                call("mlora_swap_adapters_two", *self._swap_args(other), *p._swap_args(p_other),
+                     _lib.stream(self.at.device))
+                p._swapped, self.partner, p.partner = p_other, None, None
+            else:
+                call("mlora_swap_adapters", *self._swap_args(other), _lib.stream(self.at.device))
         else:
+            other = object.__new__(_Adapters)
+            other.rank, other.padded, other.partner, other._swapped = self.rank, self.padded, None, None
             other.at = _transposed(self.bt)  # (e, R, n): B's rows become the new k
             other.bt = _transposed(self.at)  # (e, k, R)
         return other
@@ -620,13 +647,15 @@ class GateUpLink:
     (else it runs SwiGLU itself).  Backward, so that the SwiGLU backward also forms the gate_up adapter's B
     gradient (mlora_swiglu_backward_reduce): the gate_up product's forward leaves its low rows and scaling
     here, the down Function's backward leaves that gradient and the dgu it was formed from, and the gate_up
-    backward takes it when its incoming gradient is that very dgu (else it reduces as usual)."""
+    backward takes it when its incoming gradient is that very dgu (else it reduces as usual).  The gate_up
+    forward also leaves its adapters here; the down forward pairs its own with them, so the first backward
+    swaps both projections' adapters in one launch (mlora_swap_adapters_two)."""
 
     __slots__ = ("low", "scaling", "transposed", "padded", "grad_b", "dgu", "dgu_version", "want_act", "act",
-                 "act_of", "act_version")
+                 "act_of", "act_version", "adapters")
 
     def __init__(self, want_act=False):
-        self.low = self.grad_b = self.dgu = self.act = self.act_of = None
+        self.low = self.grad_b = self.dgu = self.act = self.act_of = self.adapters = None
         self.scaling, self.transposed, self.padded, self.dgu_version, self.act_version = 1.0, False, 0, -1, -1
         self.want_act = want_act
 
@@ -671,6 +700,7 @@ class _GatheredLoraProduct(torch.autograd.Function):
         ctx.link = link
         if link is not None and adapters is not None:
             link.low, link.scaling, link.transposed, link.padded = low, scaling, is_transposed, adapters.padded
+            link.adapters = adapters
         ctx.weight, ctx.adapters, ctx.scale = weight, adapters, scale
         ctx.is_transposed, ctx.scaling, ctx.k = is_transposed, scaling, k
         ctx.lhs_dtype = lhs.dtype if lhs is not None else None
@@ -798,6 +828,8 @@ class _SwigluCombinedLoraProduct(torch.autograd.Function):
             act = torch.empty((S, I2 // 2), device=gu.device, dtype=gu.dtype)
             call("mlora_swiglu", ptr(gu), S, I2 // 2, ptr(act), _lib.stream(gu.device))
         adapters = _Adapters(lhs, rhs, is_transposed) if lhs is not None else None
+        if adapters is not None and link is not None and link.adapters is not None:
+            adapters.partner, link.adapters = link.adapters, None  # swapped together in the first backward
         y, low = _launch(act, weight, scale, offsets, is_transposed, adapters, scaling, None, True)
         H = y.shape[1]
         T = inv.numel() // k

@@ -74,6 +74,8 @@ SIGNATURES = {
     "mlora_combine_backward": (c_int, [P, P, I64, P, c_int, P, I64, c_int, P, c_int, P, P, P]),
     "mlora_scale_rows": (c_int, [P, I64, I64, I64, P, c_int, P, P, I64, P]),
     "mlora_swap_adapters": (c_int, [P, I64, I64, P, I64, I64, I64, I64, I64, I64, P, P, P]),
+    "mlora_swap_adapters_two": (c_int, [P, I64, I64, P, I64, I64, I64, I64, I64, I64, P, P,
+                                        P, I64, I64, P, I64, I64, I64, I64, I64, I64, P, P, P]),
     "mlora_transpose": (c_int, [P, I64, I64, I64, I64, I64, I64, P, P]),
     "mlora_transpose_u8": (c_int, [P, I64, I64, I64, I64, I64, I64, P, P]),
     "mlora_fp8_prep": (c_int, [P, I64, I64, c_int, c_int, P, I64, P, I64, P, I64, P, I64, I64, c_int, P, I64, P, c_int,

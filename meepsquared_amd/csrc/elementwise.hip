@@ -641,20 +641,38 @@ __global__ __launch_bounds__(64) void transpose_reg_kernel(const bf16* __restric
   if (t < items) transpose_reg_item<NB>(src, A, B, s_e, s_a, dst, t);
 }
 
-// The adapters' two transposes for the input-gradient product in one launch: blocks below nb1 transpose
-// (E, N, R) -> (E, R, N) (the narrow side the source's columns), the others (E, R, K) -> (E, K, R).
-__global__ __launch_bounds__(64) void transpose_pair_kernel(const bf16* __restrict__ s1, int64_t A1, int64_t B1,
-                                                            int64_t se1, int64_t sa1, bf16* __restrict__ d1,
-                                                            int64_t items1, int64_t nb1, const bf16* __restrict__ s2,
-                                                            int64_t A2, int64_t B2, int64_t se2, int64_t sa2,
-                                                            bf16* __restrict__ d2, int64_t items2) {
-  if ((int64_t)blockIdx.x < nb1) {
-    const int64_t t = (int64_t)blockIdx.x * 64 + threadIdx.x;
-    if (t < items1) transpose_reg_item<true>(s1, A1, B1, se1, sa1, d1, t);
+// One projection's adapters swapped for the input-gradient product: bt (E, N, R) -> at_out (E, R, N) (the
+// narrow side the source's columns) over the job's first nb1 blocks, at (E, R, K) -> bt_out (E, K, R) over
+// the rest of its nb blocks.
+struct SwapJob {
+  const bf16* bt;
+  int64_t N, R, bt_se, bt_sn;
+  bf16* at_out;
+  int64_t items1, nb1;
+  const bf16* at;
+  int64_t K, at_se, at_sr;
+  bf16* bt_out;
+  int64_t items2, nb;
+};
+struct SwapJobs {
+  SwapJob j[2];  // the second one's blocks follow the first's (nb = 0: none)
+};
+
+__device__ __forceinline__ void swap_block(const SwapJob& p, int64_t b) {
+  if (b < p.nb1) {
+    const int64_t t = b * 64 + threadIdx.x;
+    if (t < p.items1) transpose_reg_item<true>(p.bt, p.N, p.R, p.bt_se, p.bt_sn, p.at_out, t);
   } else {
-    const int64_t t = ((int64_t)blockIdx.x - nb1) * 64 + threadIdx.x;
-    if (t < items2) transpose_reg_item<false>(s2, A2, B2, se2, sa2, d2, t);
+    const int64_t t = (b - p.nb1) * 64 + threadIdx.x;
+    if (t < p.items2) transpose_reg_item<false>(p.at, p.R, p.K, p.at_se, p.at_sr, p.bt_out, t);
   }
+}
+
+// The adapters' transposes for the input-gradient products of one or two projections in one launch.
+__global__ __launch_bounds__(64) void transpose_pair_kernel(SwapJobs jobs) {
+  const int64_t b = blockIdx.x;
+  if (b < jobs.j[0].nb) swap_block(jobs.j[0], b);
+  else swap_block(jobs.j[1], b - jobs.j[0].nb);
 }
 
 template <bool NB>
@@ -731,22 +749,63 @@ extern "C" int mlora_transpose_u8(const void* src, int64_t E, int64_t A, int64_t
   return launch_status("transpose_u8");
 }
 
+// Fills one projection's swap job; nonzero (the error recorded) when its shapes or strides do not fit.
+static int swap_job(const char* what, const void* at, int64_t at_se, int64_t at_sr, const void* bt, int64_t bt_se,
+                    int64_t bt_sn, int64_t E, int64_t R, int64_t K, int64_t N, void* at_out, void* bt_out,
+                    SwapJob& j) {
+  if (E < 1 || (R != 16 && R != 32) || K <= R || N <= R || K % 8 || N % 8)
+    return fail("%s: E=%lld, R=%lld, K=%lld, N=%lld: needs R 16 or 32 and K, N multiples of 8 above R", what,
+                (long long)E, (long long)R, (long long)K, (long long)N);
+  if (at_sr < K || at_sr % 8 || at_se % 8 || bt_sn < R || bt_sn % 8 || bt_se % 8 ||
+      (((uintptr_t)at | (uintptr_t)bt | (uintptr_t)at_out | (uintptr_t)bt_out) & 15u))
+    return fail("%s: the factors need 16-byte aligned rows and strides that are multiples of 8", what);
+  j.bt = (const bf16*)bt;
+  j.N = N;
+  j.R = R;
+  j.bt_se = bt_se;
+  j.bt_sn = bt_sn;
+  j.at_out = (bf16*)at_out;
+  j.items1 = E * (N / 8) * (R / 16);
+  j.nb1 = (j.items1 + 63) / 64;
+  j.at = (const bf16*)at;
+  j.K = K;
+  j.at_se = at_se;
+  j.at_sr = at_sr;
+  j.bt_out = (bf16*)bt_out;
+  j.items2 = E * (R / 16) * (K / 8);
+  j.nb = j.nb1 + (j.items2 + 63) / 64;
+  return 0;
+}
+
+static int launch_swap(const char* what, SwapJobs& jobs, void* stream) {
+  const int64_t blocks = jobs.j[0].nb + jobs.j[1].nb;
+  if (blocks > 0x7FFFFFFF) return fail("%s: the adapters exceed the grid", what);
+  hipLaunchKernelGGL(transpose_pair_kernel, dim3((unsigned)blocks), dim3(64), 0, as_stream(stream), jobs);
+  return launch_status(what);
+}
+
 extern "C" int mlora_swap_adapters(const void* at, int64_t at_se, int64_t at_sr, const void* bt, int64_t bt_se,
                                    int64_t bt_sn, int64_t E, int64_t R, int64_t K, int64_t N, void* at_out,
                                    void* bt_out, void* stream) {
   clear_error();
-  if (E < 1 || (R != 16 && R != 32) || K <= R || N <= R || K % 8 || N % 8)
-    return fail("swap_adapters: E=%lld, R=%lld, K=%lld, N=%lld: needs R 16 or 32 and K, N multiples of 8 above R",
-                (long long)E, (long long)R, (long long)K, (long long)N);
-  if (at_sr < K || at_sr % 8 || at_se % 8 || bt_sn < R || bt_sn % 8 || bt_se % 8 ||
-      (((uintptr_t)at | (uintptr_t)bt | (uintptr_t)at_out | (uintptr_t)bt_out) & 15u))
-    return fail("swap_adapters: the factors need 16-byte aligned rows and strides that are multiples of 8");
-  const int64_t items1 = E * (N / 8) * (R / 16), items2 = E * (R / 16) * (K / 8);
-  const int64_t nb1 = (items1 + 63) / 64, blocks = nb1 + (items2 + 63) / 64;
-  if (blocks > 0x7FFFFFFF) return fail("swap_adapters: (E=%lld, K=%lld, N=%lld) exceeds the grid", (long long)E,
-                                       (long long)K, (long long)N);
-  hipLaunchKernelGGL(transpose_pair_kernel, dim3((unsigned)blocks), dim3(64), 0, as_stream(stream), (const bf16*)bt, N,
-                     R, bt_se, bt_sn, (bf16*)at_out, items1, nb1, (const bf16*)at, R, K, at_se, at_sr, (bf16*)bt_out,
-                     items2);
-  return launch_status("swap_adapters");
+  SwapJobs jobs = {};
+  if (int rc = swap_job("swap_adapters", at, at_se, at_sr, bt, bt_se, bt_sn, E, R, K, N, at_out, bt_out, jobs.j[0]))
+    return rc;
+  return launch_swap("swap_adapters", jobs, stream);
+}
+
+extern "C" int mlora_swap_adapters_two(const void* at, int64_t at_se, int64_t at_sr, const void* bt, int64_t bt_se,
+                                       int64_t bt_sn, int64_t E, int64_t R, int64_t K, int64_t N, void* at_out,
+                                       void* bt_out, const void* at2, int64_t at2_se, int64_t at2_sr, const void* bt2,
+                                       int64_t bt2_se, int64_t bt2_sn, int64_t E2, int64_t R2, int64_t K2,
+                                       int64_t N2, void* at2_out, void* bt2_out, void* stream) {
+  clear_error();
+  SwapJobs jobs = {};
+  if (int rc = swap_job("swap_adapters_two", at, at_se, at_sr, bt, bt_se, bt_sn, E, R, K, N, at_out, bt_out,
+                        jobs.j[0]))
+    return rc;
+  if (int rc = swap_job("swap_adapters_two (second)", at2, at2_se, at2_sr, bt2, bt2_se, bt2_sn, E2, R2, K2, N2,
+                        at2_out, bt2_out, jobs.j[1]))
+    return rc;
+  return launch_swap("swap_adapters_two", jobs, stream);
 }

@@ -309,6 +309,35 @@ def test_the_swapped_adapters_in_one_launch_are_the_transposes(rank, K, N):
     assert torch.equal(sw.at, a.bt.transpose(1, 2)) and torch.equal(sw.bt, a.at.transpose(1, 2))
 
 
+def test_two_projections_swapped_in_one_launch_are_the_transposes(monkeypatch):
+    """mlora_swap_adapters_two: adapters paired as the layer pairs its down and gate_up adapters are both
+    swapped by the first swapped() call, in one launch, exactly the transposes; the partner's result is
+    taken once, and a later call swaps afresh."""
+    from meepsquared_amd import _grouped
+
+    torch.manual_seed(3)
+    E = 5
+    a = _grouped._Adapters(torch.randn(E, 2048, 16, device="cuda"), torch.randn(E, 16, 768, device="cuda"), False)
+    b = _grouped._Adapters(torch.randn(E, 1536, 20, device="cuda"), torch.randn(E, 20, 2048, device="cuda"), False)
+    a.partner = b
+    names = []
+    real_call = _grouped.call
+
+    def call(name, *args):
+        names.append(name)
+        return real_call(name, *args)
+
+    monkeypatch.setattr(_grouped, "call", call)
+    sa = a.swapped()
+    sb = b.swapped()
+    assert names == ["mlora_swap_adapters_two"], names
+    for x, sx in ((a, sa), (b, sb)):
+        assert torch.equal(sx.at, x.bt.transpose(1, 2)) and torch.equal(sx.bt, x.at.transpose(1, 2))
+    assert sb.padded == 32 and sb.rank == 20 and a.partner is None and b._swapped is None
+    again = b.swapped()
+    assert names[-1] == "mlora_swap_adapters" and again is not sb and torch.equal(again.at, sb.at)
+
+
 def test_the_swapped_adapters_take_each_others_roles():
     from meepsquared_amd import _grouped
 
