@@ -336,6 +336,13 @@ def test_two_projections_swapped_in_one_launch_are_the_transposes(monkeypatch):
     assert sb.padded == 32 and sb.rank == 20 and a.partner is None and b._swapped is None
     again = b.swapped()
     assert names[-1] == "mlora_swap_adapters" and again is not sb and torch.equal(again.at, sb.at)
+    # a second projection of rank 8 (not padded to 16 or 32) is refused, naming which one
+    from meepsquared_amd._lib import KernelError
+    c = _grouped._Adapters(torch.randn(E, 64, 8, device="cuda"), torch.randn(E, 8, 64, device="cuda"), False)
+    c.at, c.bt = c.at[:, :8].contiguous(), c.bt[:, :, :8].contiguous()
+    sa, sc = a._empty_swapped(), c._empty_swapped()
+    with pytest.raises(KernelError, match="second"):
+        real_call("mlora_swap_adapters_two", *a._swap_args(sa), *c._swap_args(sc), None)
 
 
 def test_the_swapped_adapters_take_each_others_roles():
