@@ -194,3 +194,52 @@ def test_swiglu_and_its_backward_are_within_one_bf16_step_of_the_exact_values():
         assert bool(((off <= _bf16_ulp(exact)) | (w.abs() < 2.0 ** -100)).all()), (name, off.max().item())
         # the random columns: a rounding of the fp32 chain lands past a bf16 midpoint only rarely
         assert (off[:, special.numel():] != 0).double().mean().item() < 2e-3, name
+
+
+@pytest.mark.parametrize("stack", ["bf16", "nf4"])
+def test_the_layer_with_swiglu_in_the_product_is_bit_identical_to_the_separate_pass(stack, monkeypatch):
+    """SwiGLU formed in the gate_up product's epilogue (the default) and the separate mlora_swiglu pass
+    (MEEPSQUARED_FUSED_SWIGLU=0) give the routed layer the same output and the same gradients, bit for bit:
+    act is formed from the same stored bf16 gate and up values either way."""
+    from meepsquared_amd import Experts, _grouped, _nf4, routed_forward, topk_softmax
+
+    torch.manual_seed(9)
+    T, H, I, E, k, r = 640, 256, 256, 8, 2, 16
+    dev = "cuda"
+    h = torch.randn(T, H, device=dev).bfloat16()
+    logits = torch.randn(T, E, device=dev).bfloat16()
+    gu = (torch.randn(E, 2 * I, H, device=dev) * 0.05).bfloat16()
+    dn = (torch.randn(E, H, I, device=dev) * 0.05).bfloat16()
+    if stack == "nf4":
+        gu, dn = _nf4.quantize_stack(gu.float()), _nf4.quantize_stack(dn.float())
+    f = {"gate_up_proj": ((torch.randn(E, 2 * I, r, device=dev) * 0.1).bfloat16(),
+                          (torch.randn(E, r, H, device=dev) * 0.1).bfloat16(), 2.0),
+         "down_proj": ((torch.randn(E, H, r, device=dev) * 0.1).bfloat16(),
+                       (torch.randn(E, r, I, device=dev) * 0.1).bfloat16(), 2.0)}
+    dy = torch.randn(T, H, device=dev).bfloat16()
+    names = []
+    real_call = _grouped.call
+
+    def call(name, *args):
+        names.append(name)
+        return real_call(name, *args)
+
+    monkeypatch.setattr(_grouped, "call", call)
+
+    def run(fused):
+        monkeypatch.setenv("MEEPSQUARED_FUSED_SWIGLU", "1" if fused else "0")
+        names.clear()
+        hh = h.clone().requires_grad_()
+        ff = {n: (a.clone().requires_grad_(), b.clone().requires_grad_(), s) for n, (a, b, s) in f.items()}
+        w, idx = topk_softmax(logits, k)
+        w = w.detach().requires_grad_()
+        out = routed_forward(Experts(gu, dn), hh, idx, w, ff)
+        out.backward(dy)
+        return [out.detach(), hh.grad, w.grad] + [t.grad for (a, b, _) in ff.values() for t in (a, b)], list(names)
+
+    got, got_names = run(True)
+    want, want_names = run(False)
+    assert "mlora_grouped_gemm_gather_swiglu" in got_names and "mlora_swiglu" not in got_names
+    assert "mlora_swiglu" in want_names and "mlora_grouped_gemm_gather_swiglu" not in want_names
+    for i, (a, b) in enumerate(zip(got, want)):
+        assert torch.equal(a, b), i
