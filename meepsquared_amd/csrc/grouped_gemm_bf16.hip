@@ -179,6 +179,19 @@ __device__ __forceinline__ int first_above(const int* v, int E, int t) {  // the
 
 // work item (tile t, column block) -> wave-uniform expert, rows and columns; small: t counts the
 // small last tiles
+// Launches with more than kGroupNb column blocks take their full tiles' items in groups of kGroupRows row
+// tiles, column block by column block: the workgroups of one XCD then run a few column blocks of several row
+// tiles at a time, each stack tile shared by up to kGroupRows items, instead of one row tile against as many
+// column blocks (as many distinct stack tiles per stage as workgroups).  A permutation of [0, T nb): group g
+// holds rows = min(kGroupRows, T - g kGroupRows) row tiles, its r-th item is column block r / rows of row
+// tile g kGroupRows + r % rows.
+constexpr int kGroupRows = 8, kGroupNb = 16;  // (at 16 column blocks the row-tile order measured faster)
+__device__ __forceinline__ int64_t grouped_item(int64_t item, int64_t T, int nb) {
+  const int64_t gsz = (int64_t)kGroupRows * nb, g = item / gsz, r = item - g * gsz;
+  const int64_t rows = min((int64_t)kGroupRows, T - g * kGroupRows), c = r / rows;
+  return (g * kGroupRows + (r - c * rows)) * nb + c;
+}
+
 __device__ __forceinline__ Item decode(const GemmArgs& p, int64_t item, int nb, const int* tend, const int* sfx,
                                        bool small, bool tall, bool tall2) {
   const int t = (int)(item / nb);
@@ -928,7 +941,8 @@ __global__ __launch_bounds__(kThreads, MLORA_DMA_OCC) void grouped_gemm_bf16_ker
 
   for (int64_t j = wg_slot; j < bcnt + scnt; j += per_xcd) {
     const bool small = j >= bcnt;
-    const int64_t item = small ? sbeg + (j - bcnt) : bbeg + j;
+    int64_t item = small ? sbeg + (j - bcnt) : bbeg + j;
+    if (!small && nb > kGroupNb) item = grouped_item(item, nbig / nb, nb);
     // the thread index taken afresh for every item: values derived from it are computed where they
     // are used, not hoisted out of this loop to hold registers through every K loop and epilogue
     int tid = tid0;

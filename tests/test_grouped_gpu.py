@@ -123,16 +123,18 @@ def test_the_product_with_adapters_and_its_gradients_match_pytorch(is_transposed
 
 
 @pytest.mark.parametrize("is_transposed", [False, True])
-def test_tall_items_match_one_product_per_expert(is_transposed):
+@pytest.mark.parametrize("N", [320, 4400])  # 4400: 18 column blocks, the items taken in groups of row tiles
+def test_tall_items_match_one_product_per_expert(is_transposed, N):
     """Groups whose last tile holds at most 32 rows past a full one (257, 288, 513, 544, 800, 1300 rows) are
     run as one item of up to 288 rows; a remainder of at most 32 n rows past n >= 2 full tiles (545, 560, 576,
     801, 832, 864, 1100, 2000, 2100 rows) is spread over the last ceil(rem / 32) tiles, each of up to 288 rows;
     289, 577, 865 and 1535 rows keep a tile of their own.  Output, input gradient and both adapter gradients
-    against the oracle, with a bias and a column block cut short (N = 320)."""
+    against the oracle, with a bias and a column block cut short (N = 320, and N = 4400, whose 18 column
+    blocks the product takes in groups of row tiles)."""
     torch.manual_seed(0)
     rows_per_expert = [257, 288, 289, 0, 545, 544, 513, 256, 1, 800, 33, 290, 560, 576, 577, 801, 832, 833, 864,
                        865, 1100, 1300, 1535, 2000, 2100]
-    K, N, rank = 160, 320, 16
+    K, rank = 160, 16
     experts = len(rows_per_expert)
     offsets = offsets_of(rows_per_expert)
     x = torch.randn(sum(rows_per_expert), K, device="cuda", dtype=torch.bfloat16).requires_grad_()
