@@ -185,7 +185,7 @@ __device__ __forceinline__ int first_above(const int* v, int E, int t) {  // the
 // column blocks (as many distinct stack tiles per stage as workgroups).  A permutation of [0, T nb): group g
 // holds rows = min(kGroupRows, T - g kGroupRows) row tiles, its r-th item is column block r / rows of row
 // tile g kGroupRows + r % rows.
-constexpr int kGroupRows = 8, kGroupNb = 16;  // (at 16 column blocks the row-tile order measured faster)
+constexpr int kGroupRows = 4, kGroupNb = 16;  // (4 measured faster than 2 or 8; at 16 column blocks the row-tile order)
 __device__ __forceinline__ int64_t grouped_item(int64_t item, int64_t T, int nb) {
   const int64_t gsz = (int64_t)kGroupRows * nb, g = item / gsz, r = item - g * gsz;
   const int64_t rows = min((int64_t)kGroupRows, T - g * kGroupRows), c = r / rows;
